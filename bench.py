@@ -1,0 +1,218 @@
+#!/usr/bin/env python3
+"""Benchmark of the 2-simplicial attention hot path on one MI355X.
+
+Prints ONE JSON line.  Headline (``value``): bf16 2-simplicial prefill
+forward throughput in TFLOP/s on the north-star shape (B=2, H=16, S=8192,
+D=128, long window w1=512, short window w2=32), effective FLOPs
+4*B*H*S*w1*w2*D, with inputs resident in HBM.  The same line carries the
+paged decode leg (tok/s and HBM GB/s), the roofline
+fraction of the dominant kernel and the CPU baseline (the oracle timed on
+this host's cores on a bounded sample of the same workload).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--legs prefill,decode,cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "next-gen-arch_amd"))
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+
+def _args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--decode-steps", type=int, default=200)
+    ap.add_argument("--legs", default="prefill,decode,cpu")
+    ap.add_argument("--workload", default="NS", help="prefill workload: NS, C2, C3, C4")
+    ap.add_argument("--cpu-positions", type=int, default=256)
+    return ap.parse_args()
+
+
+def _time_kernel(fn, steps, warmup, flush=None):
+    """Average device time per call (HIP events on the launch stream) plus wall time."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    times = []
+    wall0 = time.perf_counter()
+    if flush is None:
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            fn()
+        end.record(stream)
+        torch.cuda.synchronize()
+        times = [start.elapsed_time(end) / steps] * steps
+    else:
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        for s, e in evs:
+            flush()
+            s.record(stream)
+            fn()
+            e.record(stream)
+        torch.cuda.synchronize()
+        times = [s.elapsed_time(e) for s, e in evs]
+    wall = time.perf_counter() - wall0
+    return statistics.fmean(times), statistics.median(times), wall
+
+
+def prefill_leg(args):
+    import torch
+    from archlab_amd import simplicial_attention, simplicial_varlen_attention
+    from archlab_amd import workloads as W
+    cfg = {"NS": W.NS, "C2": W.C2, "C3": W.C3, "C4": W.C4}[args.workload]
+    dev = torch.device("cuda:0")
+    q, k1, k2, v1, v2, cu = W.prefill_inputs(cfg, device=dev)
+    if cu is None:
+        def fn():
+            return simplicial_attention(q, k1, k2, v1, v2, cfg.w2, cfg.w1, scale=1.0, return_lse=True,
+                                        kernel="mfma")
+    else:
+        def fn():
+            return simplicial_varlen_attention(q, k1, k2, v1, v2, cu, cfg.w2, cfg.w1, scale=1.0,
+                                               return_lse=True, kernel="mfma")
+    mean_ms, med_ms, _ = _time_kernel(fn, args.steps, args.warmup)
+    flops = W.prefill_flops(cfg)
+    tflops = flops / (mean_ms * 1e-3) / 1e12
+    return {
+        "cfg": cfg, "ms": mean_ms, "median_ms": med_ms, "tflops": tflops, "flops": flops,
+        "bytes": W.prefill_bytes(cfg),
+    }
+
+
+def decode_leg(args):
+    import torch
+    from archlab_amd import simplicial_paged_attention
+    from archlab_amd import workloads as W
+    from archlab_amd.architectures.simplicial_paged import paged_plan
+    cfg = W.C5
+    dev = torch.device("cuda:0")
+    inp = W.paged_inputs(cfg, device=dev)
+    a = (inp["q"], inp["short_cache"], inp["long_cache"], inp["block_table"], inp["token_seq"], inp["token_pos"])
+    kw = dict(short_window=cfg.w2, long_window=cfg.w1, scale=1.0)
+    name, splits, ws_bytes = paged_plan(*a, **kw)
+    # reuse one workspace-free call path: the shim allocates from torch's caching allocator
+    flush_buf = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device=dev)
+
+    def flush():
+        flush_buf.fill_(1)
+
+    def fn():
+        return simplicial_paged_attention(*a, return_lse=True, **kw)
+    mean_ms, med_ms, _ = _time_kernel(fn, args.decode_steps, max(args.warmup, 10), flush=flush)
+    nbytes = W.paged_bytes(cfg, inp["ctx"], out_bytes=4)
+    gbs = nbytes / (mean_ms * 1e-3) / 1e9
+    res = {
+        "workload": cfg.name, "tokens_per_step": cfg.batch, "us_per_step": mean_ms * 1e3,
+        "median_us_per_step": med_ms * 1e3, "tok_per_s": cfg.batch / (mean_ms * 1e-3),
+        "algorithmic_bytes_per_step": nbytes, "achieved_gbs": gbs, "hbm_frac": gbs / PEAK_HBM_GBS,
+        "kernel": name, "splits": splits, "flops_per_step": W.paged_flops(cfg, inp["ctx"]),
+        "l2_flushed": True,
+    }
+    del inp, flush_buf
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_leg(args, cfg):
+    """Oracle (fp32 restatement of reference_simplicial) on evenly spaced query positions."""
+    import torch
+    from archlab_amd import workloads as W
+    from oracle import simplicial_oracle as O
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    q, k1, k2, v1, v2, cu = W.prefill_inputs(cfg, device="cpu")
+    x = [t.float() for t in (q, k1, k2, v1, v2)]
+    s = cfg.seqlen
+    n = max(6, min(args.cpu_positions, s))
+    edges = {0, cfg.w2 - 1, cfg.w2, cfg.w1 - 1, cfg.w1, s - 1}
+    pos = sorted(set(int(round(i * (s - 1) / (n - 1))) for i in range(n)) | {e for e in edges if 0 <= e < s})
+    if cu is not None:
+        raise ValueError("cpu leg expects a dense workload")
+    O.reference_simplicial(*x, cfg.w2, cfg.w1, scale=1.0, query_positions=pos[:4])  # warm-up
+    runs = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        O.reference_simplicial(*x, cfg.w2, cfg.w1, scale=1.0, query_positions=pos, return_lse=True)
+        runs.append(time.perf_counter() - t0)
+    med = statistics.median(runs)
+    # nominal FLOPs of the sampled queries (same 4*B*H*w1*w2*D per query as the GPU figure)
+    flops = 4.0 * cfg.batch * cfg.heads_q * cfg.w1 * cfg.w2 * cfg.dim * len(pos)
+    per_query = med / len(pos)
+    return {
+        "value": flops / med / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+        "sample": (f"oracle.reference_simplicial fp32 on {len(pos)} evenly spaced query positions "
+                   f"(incl. window edges) of {cfg.name}, all B*H rows, median of 3; "
+                   f"{per_query * 1e3:.2f} ms/query; full {cfg.seqlen}-query run extrapolated to "
+                   f"{per_query * cfg.seqlen:.1f} s"),
+    }
+
+
+def main():
+    args = _args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no ROCm GPU visible"}))
+        sys.exit(1)
+    legs = set(args.legs.split(","))
+    from archlab_amd import workloads as W
+    out = {
+        "metric": "2-simplicial fwd TFLOP/s + % bf16 MFMA peak (S=8k,D=128); decode tok/s",
+        "value": None, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (seeded N(0,1), Q scaled 1/sqrt(D), scale=1.0)",
+    }
+    pre = None
+    if "prefill" in legs:
+        pre = prefill_leg(args)
+        cfg = pre["cfg"]
+        out["value"] = round(pre["tflops"], 2)
+        out["ms_per_step"] = round(pre["ms"], 4)
+        out["config"] = {
+            "workload": f"{cfg.name}: bf16 prefill B={cfg.batch} H={cfg.heads_q}/{cfg.heads_kv} "
+                        f"S={cfg.seqlen} D={cfg.dim} w1(long)={cfg.w1} w2(short)={cfg.w2}"
+                        + (f" varlen {cfg.varlen_seqs} seqs" if cfg.varlen_seqs else ""),
+            "flops_per_step": pre["flops"], "kernel": "prefill_mfma_kernel",
+        }
+        out["roofline"] = {
+            "bound": "mfma", "achieved": round(pre["tflops"], 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(pre["tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": None,
+        }
+    if "decode" in legs:
+        dec = decode_leg(args)
+        out["decode"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dec.items()}
+        if pre is None:
+            out["value"] = round(dec["tok_per_s"], 1)
+            out["unit"] = "tok/s"
+            out["ms_per_step"] = round(dec["us_per_step"] / 1e3, 5)
+            out["config"] = {"workload": dec["workload"]}
+            out["roofline"] = {"bound": "hbm", "achieved": round(dec["achieved_gbs"], 1), "peak": PEAK_HBM_GBS,
+                               "unit": "GB/s", "frac": round(dec["hbm_frac"], 4), "traffic": None}
+    if "cpu" in legs:
+        cfg = pre["cfg"] if pre is not None and not pre["cfg"].varlen_seqs else W.NS
+        out["cpu_baseline"] = cpu_leg(args, cfg)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,145 @@
+/*
+ * C ABI of the MI355X (gfx950) 2-simplicial attention library
+ * (libsimplicial_mi355x.so).
+ *
+ * The reference exposes this path only as Python functions over torch
+ * tensors whose kernels are Triton JIT code; there is no native FFI to mirror.
+ * Each entry point below replaces the kernel launch that sits behind one of
+ * those functions, so a host shim keeping the reference's Python signatures
+ * can call it with plain device pointers:
+ *
+ *   sa_prefill_fwd            replaces SimplicialFunction.forward / _forward
+ *                             (archlab/architectures/simplicial_kernels.py:109-131, :16-52)
+ *                             behind simplicial_attention (simplicial_attention.py:77-97);
+ *                             with cu_seqlens != NULL it is the packed
+ *                             variable-length form ("same-document" visibility,
+ *                             recipes/deepseek_v41/proposals.yaml:76).
+ *   sa_paged_fwd              replaces the _paged launch plus the torch split
+ *                             merge (simplicial_paged.py:105-128) behind
+ *                             simplicial_paged_attention (simplicial_paged.py:68-128).
+ *   sa_paged_workspace_bytes  size of the split partials that the reference
+ *                             allocates with torch.empty/full/zeros
+ *                             (simplicial_paged.py:112-114).
+ *
+ * Conventions
+ *   - All pointers are device pointers; strides are in ELEMENTS; the last
+ *     dimension of every tensor is contiguous (stride 1).
+ *   - Score operands (q, k1, k2) have head_dim D, values (v1, v2, out) have
+ *     value_dim DV.  Query head h reads KV head h / (heads_q / heads_kv).
+ *   - (k1, v1, short_window) is the short key axis, (k2, v2, long_window) the
+ *     long one (reference argument order and names).
+ *   - The library never allocates or frees device memory and never reads
+ *     device memory back to the host: every launch is asynchronous on the
+ *     given stream and can be captured into a hipGraph.
+ *   - Return value 0 = success; otherwise an SA_ERR_* code, with a message
+ *     available from sa_last_error() (thread-local).
+ */
+#ifndef SIMPLICIAL_MI355X_H
+#define SIMPLICIAL_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* sa_stream_t; /* a hipStream_t; NULL = default stream */
+
+enum {
+  SA_OK = 0,
+  SA_ERR_INVALID = 1,     /* argument / geometry check failed (ValueError) */
+  SA_ERR_UNSUPPORTED = 2, /* valid but not implemented shape/dtype (ValueError) */
+  SA_ERR_HIP = 3          /* HIP runtime error at launch (RuntimeError) */
+};
+
+enum { SA_DTYPE_F32 = 0, SA_DTYPE_BF16 = 1 };
+enum { SA_INDEX_I32 = 0, SA_INDEX_I64 = 1 };
+
+enum {
+  SA_FLAG_FORCE_GENERIC = 1 /* use the portable (non-MFMA) kernel; for cross-checks */
+};
+
+typedef struct sa_prefill_args {
+  const void* q;  /* [tokens, heads_q, D]   dtype */
+  const void* k1; /* [tokens, heads_kv, D]  dtype */
+  const void* k2; /* [tokens, heads_kv, D]  dtype */
+  const void* v1; /* [tokens, heads_kv, DV] dtype */
+  const void* v2; /* [tokens, heads_kv, DV] dtype */
+  void* out;      /* [tokens, heads_q, DV]  dtype */
+  float* lse;     /* [tokens, heads_q] fp32 natural-log LSE, or NULL */
+  const int32_t* cu_seqlens; /* [num_seqs + 1] token offsets (varlen), or NULL (dense) */
+  int64_t q_stride_t, q_stride_h;
+  int64_t k_stride_t, k_stride_h; /* shared by k1 and k2 */
+  int64_t v_stride_t, v_stride_h; /* shared by v1 and v2 */
+  int64_t o_stride_t, o_stride_h;
+  int64_t lse_stride_t;           /* lse[t * lse_stride_t + h] */
+  int32_t num_seqs;     /* dense: batch; varlen: number of sequences */
+  int32_t seqlen;       /* dense: tokens per sequence; varlen: ignored */
+  int32_t total_tokens; /* dense: batch * seqlen; varlen: cu_seqlens[num_seqs] */
+  int32_t heads_q, heads_kv, head_dim, value_dim;
+  int32_t short_window, long_window;
+  float scale;
+  int32_t dtype; /* SA_DTYPE_* of every tensor except lse */
+  int32_t flags; /* SA_FLAG_* */
+} sa_prefill_args;
+
+typedef struct sa_paged_args {
+  const void* q; /* [tokens, heads_q, D], q_dtype */
+  int64_t q_stride_t, q_stride_h;
+  const void* short_cache; /* [2 (K,V), blocks, block_size, heads_kv, D], cache_dtype */
+  int64_t sc_stride[4];    /* element strides of dims 0..3 */
+  const void* long_cache;
+  int64_t lc_stride[4];
+  const void* short_table; /* [num_seqs, short_table_width] of index_dtype */
+  int64_t st_stride;
+  const void* long_table;  /* [num_seqs, long_table_width]; may equal short_table */
+  int64_t lt_stride;
+  const void* token_seq; /* [tokens] index_dtype */
+  const void* token_pos; /* [tokens] index_dtype */
+  float* out;            /* [tokens, heads_q, D] fp32 */
+  int64_t o_stride_t, o_stride_h;
+  float* lse;            /* [tokens, heads_q] fp32 natural log, or NULL */
+  int32_t tokens, heads_q, heads_kv, head_dim, block_size;
+  int32_t num_seqs;                 /* rows of both tables */
+  int32_t short_table_width, long_table_width;
+  int32_t short_blocks, long_blocks; /* dim 1 of each cache; table entries are clamped to it */
+  int32_t short_window, long_window;
+  int32_t splits;        /* long-window splits; <= 0 selects automatically */
+  float scale;
+  int32_t q_dtype, cache_dtype; /* SA_DTYPE_* */
+  int32_t table_index_dtype, token_index_dtype; /* SA_INDEX_* */
+  int32_t flags;
+} sa_paged_args;
+
+/* Dense or packed-varlen prefill forward: out and (optionally) lse. */
+int sa_prefill_fwd(const sa_prefill_args* args, sa_stream_t stream);
+
+/* Bytes of device workspace sa_paged_fwd needs for these arguments. */
+size_t sa_paged_workspace_bytes(const sa_paged_args* args);
+
+/* Paged forward for any mix of prefill and decode tokens; workspace must hold
+ * sa_paged_workspace_bytes(args) bytes (256-byte aligned). */
+int sa_paged_fwd(const sa_paged_args* args, void* workspace, size_t workspace_bytes,
+                 sa_stream_t stream);
+
+/* Splits the paged launch would use for these arguments (after auto-selection). */
+int sa_paged_splits(const sa_paged_args* args);
+
+/* Name of the kernel family a call with these arguments runs: "mfma" (bf16
+ * matrix-core path) or "generic" (portable path, fp32 and other shapes);
+ * NULL if the arguments are invalid. */
+const char* sa_prefill_kernel(const sa_prefill_args* args);
+const char* sa_paged_kernel(const sa_paged_args* args);
+
+/* Message describing the last failed call on this thread ("" if none). */
+const char* sa_last_error(void);
+
+/* Library version string. */
+const char* sa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SIMPLICIAL_MI355X_H */

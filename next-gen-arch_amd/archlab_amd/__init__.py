@@ -1,0 +1,22 @@
+"""MI355X-native 2-simplicial (trilinear) sliding-window attention.
+
+Forward-path drop-in for archlab's ``simplicial_attention`` and
+``simplicial_paged_attention``; the kernels are hand-written gfx950 HIP behind
+the C ABI of ``include/simplicial_mi355x.h``.
+"""
+
+from .architectures.simplicial_attention import (  # noqa: F401
+    simplicial_attention,
+    simplicial_varlen_attention,
+    validate_inputs,
+)
+from .architectures.simplicial_paged import simplicial_paged_attention  # noqa: F401
+from .serving import token_layout  # noqa: F401
+
+__all__ = [
+    "simplicial_attention",
+    "simplicial_varlen_attention",
+    "simplicial_paged_attention",
+    "validate_inputs",
+    "token_layout",
+]

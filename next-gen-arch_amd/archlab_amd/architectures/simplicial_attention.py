@@ -1,0 +1,184 @@
+"""2-simplicial (trilinear) sliding-window attention on MI355X: prefill forms.
+
+Drop-in for ``archlab.architectures.simplicial_attention`` on the forward
+path.  Tensor layout is [batch, sequence, heads, head_dim]; the score is
+``scale * sum_d q_i[d] * k1_j[d] * k2_k[d]`` with ``j`` in the causal short
+window and ``k`` in the causal long window, one joint softmax over all valid
+(j, k) pairs, and the output ``sum_jk P_ijk * (v1_j ⊙ v2_k)``.
+
+The computation runs in hand-written gfx950 HIP kernels
+(``libsimplicial_mi355x.so``, C ABI in ``include/simplicial_mi355x.h``); this
+module only validates, allocates outputs with torch's caching allocator and
+passes pointers.  There is no CPU path here: non-GPU tensors raise, exactly
+as the reference does.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from numbers import Real
+
+import torch
+
+from .. import _native
+
+
+def validate_inputs(q, k1, k2, v1, v2, short_window, long_window, *,
+                    allow_scaled_query=False, allow_value_dim=False):
+    """Contract checks with the reference's messages (simplicial_attention.py:17-38)."""
+    if q.ndim != 4 or any(x.ndim != 4 for x in (k1, k2, v1, v2)):
+        raise ValueError("expected [batch, sequence, heads, head_dim]")
+    if min(short_window, long_window) < 1 or short_window > long_window:
+        raise ValueError("require 1 <= short_window <= long_window")
+    b, n, heads, d = q.shape
+    if min(b, n, heads, d) < 1:
+        raise ValueError("empty attention dimensions are unsupported")
+    if k2.shape != k1.shape or v2.shape != v1.shape or v1.shape[:3] != k1.shape[:3]:
+        raise ValueError("both key/value branches must have matching batch, sequence and heads")
+    if v1.shape[-1] < 1 or (not allow_value_dim and v1.shape[-1] != d):
+        raise ValueError("unsupported value head dimension")
+    if k1.shape[2] < 1 or k1.shape[:2] != (b, n) or k1.shape[-1] != d or heads % k1.shape[2]:
+        raise ValueError("incompatible grouped-query geometry")
+    dtype = (
+        k1.dtype
+        if allow_scaled_query and q.dtype == torch.float32 and k1.dtype == torch.bfloat16
+        else q.dtype
+    )
+    if any(x.dtype != dtype or x.device != q.device for x in (k1, k2, v1, v2)):
+        raise ValueError("all inputs must have the same dtype and device")
+
+
+def _score_scale(scale, dim):
+    """simplicial_attention.py:41-46: None -> 1/sqrt(score_dim), else a finite real."""
+    if scale is None:
+        return 1 / math.sqrt(dim)
+    if not isinstance(scale, Real) or not math.isfinite(scale):
+        raise ValueError("scale must be a finite real number")
+    return float(scale)
+
+
+def _kernel_checks(q, v_dim, score_dim):
+    """simplicial_attention.py:87-92 device / dtype / head-dim contract."""
+    if q.device.type != "cuda" or q.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("kernel supports CUDA float32/bfloat16")
+    if score_dim not in (16, 32, 64, 128, 256, 512):
+        raise ValueError("unsupported score head dimension")
+    if v_dim not in (16, 32, 64, 128, 256):
+        raise ValueError("unsupported value head dimension")
+
+
+def _forward_only(*tensors):
+    if torch.is_grad_enabled() and any(t.requires_grad for t in tensors):
+        raise ValueError("simplicial attention on MI355X is forward-only: no backward kernel is provided")
+
+
+def _kernel_flag(kernel):
+    if kernel not in ("auto", "mfma", "generic"):
+        raise ValueError("kernel must be 'auto', 'mfma' or 'generic'")
+    return _native.SA_FLAG_FORCE_GENERIC if kernel == "generic" else 0
+
+
+def _prefill(q, k1, k2, v1, v2, short_window, long_window, scale, cu_seqlens, num_seqs, seqlen,
+             return_lse, kernel):
+    """q [T,HQ,D], k [T,HK,D], v [T,HK,DV] contiguous -> out [T,HQ,DV], lse [T,HQ]."""
+    lib = _native.load()
+    tokens, hq, d = q.shape
+    hk, dv = k1.shape[1], v1.shape[-1]
+    if hq // hk > 128:
+        raise ValueError("at most 128 query heads per KV group")
+    out = torch.empty((tokens, hq, dv), device=q.device, dtype=q.dtype)
+    lse = torch.empty((tokens, hq), device=q.device, dtype=torch.float32) if return_lse else None
+    args = _native.PrefillArgs(
+        q=q.data_ptr(), k1=k1.data_ptr(), k2=k2.data_ptr(), v1=v1.data_ptr(), v2=v2.data_ptr(),
+        out=out.data_ptr(), lse=lse.data_ptr() if lse is not None else None,
+        cu_seqlens=cu_seqlens.data_ptr() if cu_seqlens is not None else None,
+        q_stride_t=q.stride(0), q_stride_h=q.stride(1),
+        k_stride_t=k1.stride(0), k_stride_h=k1.stride(1),
+        v_stride_t=v1.stride(0), v_stride_h=v1.stride(1),
+        o_stride_t=out.stride(0), o_stride_h=out.stride(1), lse_stride_t=hq,
+        num_seqs=num_seqs, seqlen=seqlen, total_tokens=tokens,
+        heads_q=hq, heads_kv=hk, head_dim=d, value_dim=dv,
+        short_window=int(short_window), long_window=int(long_window),
+        scale=scale, dtype=_native.dtype_code(q.dtype), flags=_kernel_flag(kernel))
+    if kernel == "mfma" and lib.sa_prefill_kernel(ctypes.byref(args)) != b"mfma":
+        raise ValueError("the MFMA kernel does not cover this dtype / head_dim / layout")
+    with torch.cuda.device(q.device):
+        _native.check(lib.sa_prefill_fwd(ctypes.byref(args), _native.stream_handle(q.device)))
+    return out, lse
+
+
+def simplicial_attention(q, k1, k2, v1, v2, short_window, long_window, *, scale=None,
+                         return_lse=False, kernel="auto"):
+    """Drop-in for ``simplicial_attention`` (simplicial_attention.py:77-97), forward only.
+
+    q [B,N,HQ,D]; k1, k2 [B,N,HK,D]; v1, v2 [B,N,HK,DV].  Returns O
+    [B,N,HQ,DV] in q's dtype and, with ``return_lse=True``, also the
+    natural-log LSE [B,N,HQ] in float32.  ``kernel`` selects the
+    implementation: "auto" (bf16 with D == DV in {64,128,256} runs on the MFMA
+    kernel, everything else on the portable kernel), "mfma" (raise if not
+    covered) or "generic".
+
+    Deviation from the reference: the forward is deterministic (no atomics),
+    so ``torch.use_deterministic_algorithms(True)`` is allowed; inputs that
+    require grad raise ValueError because no backward kernel exists.
+    """
+    validate_inputs(q, k1, k2, v1, v2, short_window, long_window, allow_value_dim=True)
+    scale = _score_scale(scale, q.shape[-1])
+    _kernel_checks(q, v1.shape[-1], q.shape[-1])
+    _forward_only(q, k1, k2, v1, v2)
+    b, n, hq, d = q.shape
+    hk, dv = k1.shape[2], v1.shape[-1]
+    q_, k1_, k2_ = (x.contiguous().view(b * n, -1, d) for x in (q, k1, k2))
+    v1_, v2_ = (x.contiguous().view(b * n, hk, dv) for x in (v1, v2))
+    out, lse = _prefill(q_, k1_, k2_, v1_, v2_, short_window, long_window, scale, None, b, n,
+                        return_lse, kernel)
+    out = out.view(b, n, hq, dv)
+    if return_lse:
+        return out, lse.view(b, n, hq)
+    return out
+
+
+def simplicial_varlen_attention(q, k1, k2, v1, v2, cu_seqlens, short_window, long_window, *,
+                                scale=None, return_lse=False, kernel="auto"):
+    """Packed variable-length prefill: q [T,HQ,D], k1/k2 [T,HK,D], v1/v2 [T,HK,DV].
+
+    ``cu_seqlens`` is int32 [num_seqs + 1] on q's device (cu[0] = 0,
+    cu[-1] = T, non-decreasing).  Each sequence is attended on its own, i.e.
+    the result equals ``simplicial_attention`` applied to every
+    ``[cu[s], cu[s+1])`` slice ("same-document" visibility,
+    recipes/deepseek_v41/proposals.yaml:76).  The offsets are not read back to
+    the host; a malformed ``cu_seqlens`` yields meaningless values but never
+    addresses memory outside the tensors.
+    """
+    if q.ndim != 3 or any(x.ndim != 3 for x in (k1, k2, v1, v2)):
+        raise ValueError("expected packed [tokens, heads, head_dim]")
+    validate_inputs(q[None], k1[None], k2[None], v1[None], v2[None], short_window, long_window,
+                    allow_value_dim=True)
+    scale = _score_scale(scale, q.shape[-1])
+    _kernel_checks(q, v1.shape[-1], q.shape[-1])
+    _forward_only(q, k1, k2, v1, v2)
+    if (cu_seqlens.ndim != 1 or cu_seqlens.dtype != torch.int32 or cu_seqlens.numel() < 2
+            or cu_seqlens.device != q.device):
+        raise ValueError("cu_seqlens must be int32 [num_seqs + 1] on the input device")
+    t, hq, d = q.shape
+    q_, k1_, k2_, v1_, v2_ = (x.contiguous() for x in (q, k1, k2, v1, v2))
+    out, lse = _prefill(q_, k1_, k2_, v1_, v2_, short_window, long_window, scale,
+                        cu_seqlens.contiguous(), cu_seqlens.numel() - 1, 0, return_lse, kernel)
+    return (out, lse) if return_lse else out
+
+
+def prefill_kernel_name(q, k1, v1, *, kernel="auto"):
+    """Which kernel family ('mfma' or 'generic') a dense call with these shapes runs."""
+    lib = _native.load()
+    b, n, hq, d = q.shape
+    args = _native.PrefillArgs(
+        q=16, k1=16, k2=16, v1=16, v2=16, out=16,
+        q_stride_t=hq * d, q_stride_h=d, k_stride_t=k1.shape[2] * d, k_stride_h=d,
+        v_stride_t=k1.shape[2] * v1.shape[-1], v_stride_h=v1.shape[-1],
+        o_stride_t=hq * v1.shape[-1], o_stride_h=v1.shape[-1], lse_stride_t=hq,
+        num_seqs=b, seqlen=n, total_tokens=b * n, heads_q=hq, heads_kv=k1.shape[2], head_dim=d,
+        value_dim=v1.shape[-1], short_window=1, long_window=1, scale=1.0,
+        dtype=_native.dtype_code(q.dtype), flags=_kernel_flag(kernel))
+    name = lib.sa_prefill_kernel(ctypes.byref(args))
+    return None if name is None else name.decode()

@@ -1,0 +1,147 @@
+// extern "C" entry points of libsimplicial_mi355x.so (declared in
+// include/simplicial_mi355x.h).  Argument checks mirror the reference's
+// ValueError contracts (simplicial_attention.py:17-38, :87-92;
+// simplicial_paged.py:78-103); the Python shim raises the same messages before
+// calling in, these checks guard C callers.
+#include <mutex>
+#include <string>
+
+#include "sa_launch.h"
+
+namespace sa {
+
+static thread_local std::string g_last_error;
+
+static int fail(int code, const char* msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int device_cu_count() {
+  static std::mutex mu;
+  static int counts[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if (counts[dev] == 0) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+    counts[dev] = c;
+  }
+  return counts[dev];
+}
+
+static bool pow2_dim(int d, int lo, int hi) { return d >= lo && d <= hi && (d & (d - 1)) == 0; }
+
+static int check_prefill(const sa_prefill_args* a) {
+  if (!a) return fail(SA_ERR_INVALID, "null arguments");
+  if (!a->q || !a->k1 || !a->k2 || !a->v1 || !a->v2 || !a->out) return fail(SA_ERR_INVALID, "null tensor pointer");
+  if (a->short_window < 1 || a->long_window < a->short_window)
+    return fail(SA_ERR_INVALID, "require 1 <= short_window <= long_window");
+  if (a->heads_q < 1 || a->heads_kv < 1 || a->head_dim < 1 || a->value_dim < 1 || a->num_seqs < 1)
+    return fail(SA_ERR_INVALID, "empty attention dimensions are unsupported");
+  if (a->heads_q % a->heads_kv) return fail(SA_ERR_INVALID, "incompatible grouped-query geometry");
+  if (a->heads_q / a->heads_kv > 128) return fail(SA_ERR_INVALID, "at most 128 query heads per KV group");
+  if (!pow2_dim(a->head_dim, 16, 512)) return fail(SA_ERR_INVALID, "unsupported score head dimension");
+  if (!pow2_dim(a->value_dim, 16, 256)) return fail(SA_ERR_INVALID, "unsupported value head dimension");
+  if (a->dtype != SA_DTYPE_F32 && a->dtype != SA_DTYPE_BF16)
+    return fail(SA_ERR_INVALID, "kernel supports float32/bfloat16");
+  if (a->cu_seqlens == nullptr) {
+    if (a->seqlen < 1 || (int64_t)a->seqlen * a->num_seqs != a->total_tokens)
+      return fail(SA_ERR_INVALID, "dense layout needs total_tokens == num_seqs * seqlen");
+  }
+  if (a->total_tokens < 0) return fail(SA_ERR_INVALID, "negative token count");
+  return SA_OK;
+}
+
+static bool mfma_prefill_ok(const sa_prefill_args* a) {
+  if (a->flags & SA_FLAG_FORCE_GENERIC) return false;
+  if (a->dtype != SA_DTYPE_BF16) return false;
+  if (a->head_dim != a->value_dim) return false;
+  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256) return false;
+  const int64_t st[] = {a->q_stride_t, a->q_stride_h, a->k_stride_t, a->k_stride_h,
+                        a->v_stride_t, a->v_stride_h, a->o_stride_t, a->o_stride_h};
+  for (int64_t s : st)
+    if (s % 8) return false;
+  const uintptr_t ptrs = (uintptr_t)a->q | (uintptr_t)a->k1 | (uintptr_t)a->k2 | (uintptr_t)a->v1 |
+                         (uintptr_t)a->v2 | (uintptr_t)a->out;
+  return (ptrs & 15) == 0;
+}
+
+static int check_paged(const sa_paged_args* a) {
+  if (!a) return fail(SA_ERR_INVALID, "null arguments");
+  if (a->tokens < 0) return fail(SA_ERR_INVALID, "negative token count");
+  if (a->short_window < 1 || a->long_window < a->short_window)
+    return fail(SA_ERR_INVALID, "require 1 <= short_window <= long_window");
+  if (a->heads_q < 1 || a->heads_kv < 1 || a->heads_q % a->heads_kv || a->block_size < 1 ||
+      !pow2_dim(a->head_dim, 16, 256))
+    return fail(SA_ERR_INVALID, "incompatible paged simplicial geometry");
+  if (a->heads_q / a->heads_kv > 128) return fail(SA_ERR_INVALID, "at most 128 query heads per KV group");
+  if ((a->q_dtype != SA_DTYPE_F32 && a->q_dtype != SA_DTYPE_BF16) ||
+      (a->cache_dtype != SA_DTYPE_F32 && a->cache_dtype != SA_DTYPE_BF16) ||
+      (a->table_index_dtype != SA_INDEX_I32 && a->table_index_dtype != SA_INDEX_I64) ||
+      (a->token_index_dtype != SA_INDEX_I32 && a->token_index_dtype != SA_INDEX_I64))
+    return fail(SA_ERR_INVALID, "invalid paged simplicial inputs");
+  if (a->tokens > 0 && (a->num_seqs < 1 || a->short_table_width < 1 || a->long_table_width < 1 ||
+                        a->short_blocks < 1 || a->long_blocks < 1))
+    return fail(SA_ERR_INVALID, "invalid paged simplicial inputs");
+  if (a->tokens > 0 && (!a->q || !a->short_cache || !a->long_cache || !a->short_table || !a->long_table ||
+                        !a->token_seq || !a->token_pos || !a->out))
+    return fail(SA_ERR_INVALID, "null tensor pointer");
+  return SA_OK;
+}
+
+}  // namespace sa
+
+extern "C" {
+
+const char* sa_last_error(void) { return sa::g_last_error.c_str(); }
+
+const char* sa_version(void) { return "simplicial_mi355x 0.1 (gfx950)"; }
+
+int sa_prefill_fwd(const sa_prefill_args* a, sa_stream_t stream) {
+  int rc = sa::check_prefill(a);
+  if (rc != SA_OK) return rc;
+  if (a->total_tokens == 0) return SA_OK;
+  hipError_t e = sa::mfma_prefill_ok(a) ? sa::launch_prefill_bf16_mfma(a, (hipStream_t)stream)
+                                        : sa::launch_prefill_generic(a, (hipStream_t)stream);
+  if (e != hipSuccess) return sa::fail(SA_ERR_HIP, hipGetErrorString(e));
+  sa::g_last_error.clear();
+  return SA_OK;
+}
+
+const char* sa_prefill_kernel(const sa_prefill_args* a) {
+  if (sa::check_prefill(a) != SA_OK) return nullptr;
+  return sa::mfma_prefill_ok(a) ? "mfma" : "generic";
+}
+
+const char* sa_paged_kernel(const sa_paged_args* a) {
+  if (sa::check_paged(a) != SA_OK) return nullptr;
+  return sa::paged_mfma_supported(a) ? "mfma" : "generic";
+}
+
+int sa_paged_splits(const sa_paged_args* a) {
+  if (sa::check_paged(a) != SA_OK) return -1;
+  return sa::paged_choose_splits(a);
+}
+
+size_t sa_paged_workspace_bytes(const sa_paged_args* a) {
+  if (sa::check_paged(a) != SA_OK) return 0;
+  return sa::paged_workspace_bytes(a, sa::paged_choose_splits(a));
+}
+
+int sa_paged_fwd(const sa_paged_args* a, void* workspace, size_t workspace_bytes, sa_stream_t stream) {
+  int rc = sa::check_paged(a);
+  if (rc != SA_OK) return rc;
+  if (a->tokens == 0) return SA_OK;
+  const int splits = sa::paged_choose_splits(a);
+  const size_t need = sa::paged_workspace_bytes(a, splits);
+  if (workspace_bytes < need) return sa::fail(SA_ERR_INVALID, "workspace too small");
+  if (need && ((uintptr_t)workspace & 255)) return sa::fail(SA_ERR_INVALID, "workspace must be 256-byte aligned");
+  hipError_t e = sa::launch_paged(a, splits, workspace, workspace_bytes, (hipStream_t)stream);
+  if (e != hipSuccess) return sa::fail(SA_ERR_HIP, hipGetErrorString(e));
+  sa::g_last_error.clear();
+  return SA_OK;
+}
+
+}  // extern "C"

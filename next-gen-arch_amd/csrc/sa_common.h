@@ -1,0 +1,109 @@
+// Shared device-side building blocks for the 2-simplicial attention kernels
+// (gfx950 / CDNA4).  Every kernel in this library computes, for a query token
+// t and a query head h (KV group g = h / G):
+//
+//   score(j, k) = scale * sum_d q_t[d] * k1_j[d] * k2_k[d]
+//   P           = one softmax over all valid (j, k) pairs
+//   out_t       = sum_{j,k} P(j, k) * (v1_j ⊙ v2_k)
+//   lse_t       = log sum_{j,k} exp(score(j, k))            (natural log)
+//
+// with j in the short window [t - short_window + 1, t] and k in the long
+// window [t - long_window + 1, t], both clipped at the start of t's sequence.
+//
+// MFMA formulation used by the bf16 kernels.  For one query token and head
+// the short window supplies up to 32 "A rows"  a_j = bf16(q_t ⊙ k1_j), and a
+// 32-key chunk of the long window is contracted as
+//
+//     S^T[key][row] = K_chunk[key][:] · a_row[:]         (v_mfma_f32_32x32x16_bf16)
+//     O^T[d][row]  += V^T[d][key] · P^T[key][row]        (same instruction)
+//
+// so that each lane of a wave owns one A row (column l % 32 of the 32x32
+// accumulator tile).  Every row keeps its own running max / sum; the joint
+// softmax of the reference is recovered exactly in the epilogue by the
+// log-sum-exp merge of the rows:  out = sum_j w_j v1_j ⊙ O_j / sum_j w_j z_j
+// with w_j = exp(m_j - max_j m_j).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sa {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kWave = 64;
+constexpr int kChunk = 32;  // keys per MFMA chunk (M dimension of the 32x32 tile)
+
+__device__ __forceinline__ float bf16_to_f32(bf16 x) { return (float)x; }
+
+// Round-to-nearest-even fp32 -> bf16 (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ bf16 f32_to_bf16(float x) { return (bf16)x; }
+
+__device__ __forceinline__ floatx16 mfma32x32x16(const bf16x8& a, const bf16x8& b, const floatx16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Row (= lane % 32) of a 32x32 accumulator tile and the tile row held in
+// register r by lane l:  row_of(r, l) = 8*(r/4) + 4*(l/32) + r%4.
+__device__ __forceinline__ int acc_row(int r, int half) { return 8 * (r >> 2) + 4 * half + (r & 3); }
+
+// Exchange a 32-bit value with the lane 32 positions away (l <-> l ^ 32).
+__device__ __forceinline__ float swap_halves(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]);
+}
+
+// xor-shuffle within groups of 32 lanes (ds_swizzle bit-mask mode, no
+// address registers): lane l reads lane l ^ m, m < 32.
+template <int M>
+__device__ __forceinline__ float swz_xor(float x) {
+  static_assert(M > 0 && M < 32, "xor mask within 32 lanes");
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x1f | (M << 10)));
+}
+
+// Max / sum over the 32 lanes that share l / 32.
+__device__ __forceinline__ float half_max(float x) {
+  x = fmaxf(x, swz_xor<16>(x));
+  x = fmaxf(x, swz_xor<8>(x));
+  x = fmaxf(x, swz_xor<4>(x));
+  x = fmaxf(x, swz_xor<2>(x));
+  return fmaxf(x, swz_xor<1>(x));
+}
+
+__device__ __forceinline__ float half_sum(float x) {
+  x += swz_xor<16>(x);
+  x += swz_xor<8>(x);
+  x += swz_xor<4>(x);
+  x += swz_xor<2>(x);
+  return x + swz_xor<1>(x);
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+  x = half_max(x);
+  return fmaxf(x, swap_halves(x));
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+  x = half_sum(x);
+  return x + swap_halves(x);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2 v;
+  v[0] = f32_to_bf16(lo);
+  v[1] = f32_to_bf16(hi);
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+}  // namespace sa

@@ -1,0 +1,213 @@
+// Portable (non-MFMA) 2-simplicial forward kernel, shared by the prefill and
+// paged entry points.  It covers every dtype / head-dim combination the
+// reference accepts (fp32 or bf16 operands, D in {16..512}, DV in {16..256})
+// and is the kernel used for fp32 inputs, where the reference's tf32x3 dots
+// (simplicial_kernels.py:42, :48) keep fp32 accuracy.
+//
+// One workgroup (256 threads) owns one (query token, query head).  Short-axis
+// rows are processed in groups of JB, long-axis keys in chunks of KB; the
+// online softmax runs over every (j, k) pair of a group x chunk at once, so the
+// joint softmax of the reference is kept exactly.  Rounding points follow the
+// reference kernel: a = (q ⊙ k1) rounded to the query dtype
+// (simplicial_kernels.py:35), P rounded to the value dtype before P·V2
+// (simplicial_kernels.py:48), fp32 accumulation.
+#pragma once
+
+#include "sa_common.h"
+
+namespace sa {
+
+template <typename T>
+__device__ __forceinline__ float ld(const T* p) { return (float)(*p); }
+
+template <typename T>
+__device__ __forceinline__ float round_to(float x) { return (float)(T)x; }
+template <>
+__device__ __forceinline__ float round_to<float>(float x) { return x; }
+
+// Where the rows of one query's key windows live.  Positions are relative to
+// the start of the query's own sequence.
+struct DenseRows {
+  const void* k1;
+  const void* k2;
+  const void* v1;
+  const void* v2;
+  int64_t k_st, k_sh, v_st, v_sh;
+  int64_t seq_base;  // global token index of position 0
+  __device__ int64_t k_off(int pos, int g) const { return (seq_base + pos) * k_st + (int64_t)g * k_sh; }
+  __device__ int64_t v_off(int pos, int g) const { return (seq_base + pos) * v_st + (int64_t)g * v_sh; }
+  __device__ int64_t k1_off(int pos, int g) const { return k_off(pos, g); }
+  __device__ int64_t k2_off(int pos, int g) const { return k_off(pos, g); }
+  __device__ int64_t v1_off(int pos, int g) const { return v_off(pos, g); }
+  __device__ int64_t v2_off(int pos, int g) const { return v_off(pos, g); }
+  __device__ const void* k1p() const { return k1; }
+  __device__ const void* k2p() const { return k2; }
+  __device__ const void* v1p() const { return v1; }
+  __device__ const void* v2p() const { return v2; }
+};
+
+__device__ __forceinline__ int64_t load_index(const void* base, int64_t i, int is64) {
+  return is64 ? ((const int64_t*)base)[i] : (int64_t)((const int32_t*)base)[i];
+}
+
+__device__ __forceinline__ int64_t clamp64(int64_t x, int64_t lo, int64_t hi) { return x < lo ? lo : (x > hi ? hi : x); }
+
+// Physical block of logical position `pos` of sequence `seq`:
+// table[seq, pos / block_size] widened to int64.  The column and the block id
+// are clamped into the table / cache so that corrupt metadata cannot address
+// memory outside them (the result for such a token is then meaningless).
+__device__ __forceinline__ int64_t block_of(const void* table, int is64, int64_t row_stride, int width, int64_t nblocks,
+                                            int64_t seq, int pos, int block_size) {
+  const int64_t col = clamp64(pos / block_size, 0, width - 1);
+  return clamp64(load_index(table, seq * row_stride + col, is64), 0, nblocks - 1);
+}
+
+// Paged caches [2 (K,V), blocks, block_size, heads_kv, D] with arbitrary
+// strides.  block = table[seq, pos / block_size] widened to int64 before the
+// stride multiply, slot = pos % block_size (simplicial_paged.py:41-44, :49-52).
+struct PagedRows {
+  const void* sc;
+  const void* lc;
+  int64_t sc_a, sc_b, sc_s, sc_h;
+  int64_t lc_a, lc_b, lc_s, lc_h;
+  const void* stable;
+  const void* ltable;
+  int64_t st_s, lt_s;
+  int table64;
+  int block_size;
+  int st_w, lt_w;
+  int64_t s_blocks, l_blocks;
+  int64_t seq;
+  __device__ int64_t s_off(int pos, int g) const {
+    const int64_t blk = block_of(stable, table64, st_s, st_w, s_blocks, seq, pos, block_size);
+    return blk * sc_b + (int64_t)(pos % block_size) * sc_s + (int64_t)g * sc_h;
+  }
+  __device__ int64_t l_off(int pos, int g) const {
+    const int64_t blk = block_of(ltable, table64, lt_s, lt_w, l_blocks, seq, pos, block_size);
+    return blk * lc_b + (int64_t)(pos % block_size) * lc_s + (int64_t)g * lc_h;
+  }
+  __device__ int64_t k1_off(int pos, int g) const { return s_off(pos, g); }
+  __device__ int64_t v1_off(int pos, int g) const { return s_off(pos, g) + sc_a; }
+  __device__ int64_t k2_off(int pos, int g) const { return l_off(pos, g); }
+  __device__ int64_t v2_off(int pos, int g) const { return l_off(pos, g) + lc_a; }
+  __device__ const void* k1p() const { return sc; }
+  __device__ const void* k2p() const { return lc; }
+  __device__ const void* v1p() const { return sc; }
+  __device__ const void* v2p() const { return lc; }
+};
+
+constexpr int kGenThreads = 256;
+constexpr int kGenJB = 16;
+
+__host__ __device__ constexpr int gen_kb(int d) { return d >= 512 ? 16 : (d >= 256 ? 32 : 64); }
+
+// Dynamic LDS bytes the generic kernel needs for score width D and value width DV.
+__host__ __device__ inline size_t gen_lds_bytes(int d, int dv) {
+  int kb = gen_kb(d);
+  size_t f = (size_t)kGenJB * (d + 1) + (size_t)kb * (d + 1) + (size_t)kGenJB * dv + (size_t)kb * dv +
+             (size_t)kGenJB * (kb + 1) + d + 64;
+  return f * sizeof(float);
+}
+
+// One (query, head): q points at the query row; writes out[DV] (OT) and lse.
+// QT: query dtype (sets the rounding points), CT: key/value dtype.
+template <typename QT, typename CT, typename OT, typename Rows>
+__device__ void generic_query(const QT* __restrict__ q, const Rows& rows, int g, int pos, int short_window,
+                              int long_window, int D, int DV, float scale, OT* __restrict__ out,
+                              float* __restrict__ lse) {
+  extern __shared__ float smem[];
+  const int KB = gen_kb(D);
+  float* As = smem;                          // [JB][D+1]
+  float* Ks = As + kGenJB * (D + 1);         // [KB][D+1]
+  float* V1s = Ks + KB * (D + 1);            // [JB][DV]
+  float* V2s = V1s + kGenJB * DV;            // [KB][DV]
+  float* Ps = V2s + KB * DV;                 // [JB][KB+1]
+  float* Qs = Ps + kGenJB * (KB + 1);        // [D]
+  float* red = Qs + D;                       // [64] reduction scratch
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
+  const CT* k1 = (const CT*)rows.k1p();
+  const CT* k2 = (const CT*)rows.k2p();
+  const CT* v1 = (const CT*)rows.v1p();
+  const CT* v2 = (const CT*)rows.v2p();
+
+  for (int d = tid; d < D; d += kGenThreads) Qs[d] = ld(q + d);
+  const int lo1 = max(0, pos - short_window + 1);
+  const int lo2 = max(0, pos - long_window + 1);
+  float m = -INFINITY, z = 0.f;
+  float acc = 0.f;  // out[tid] (DV <= 256)
+  __syncthreads();
+
+  for (int j0 = lo1; j0 <= pos; j0 += kGenJB) {
+    const int nj = min(kGenJB, pos - j0 + 1);
+    for (int e = tid; e < nj * D; e += kGenThreads) {
+      int jj = e / D, d = e % D;
+      float kv = ld(k1 + rows.k1_off(j0 + jj, g) + d);
+      As[jj * (D + 1) + d] = round_to<QT>(Qs[d] * kv);
+    }
+    for (int e = tid; e < nj * DV; e += kGenThreads) {
+      int jj = e / DV, d = e % DV;
+      V1s[jj * DV + d] = ld(v1 + rows.v1_off(j0 + jj, g) + d);
+    }
+    for (int k0 = lo2; k0 <= pos; k0 += KB) {
+      const int nk = min(KB, pos - k0 + 1);
+      __syncthreads();  // previous chunk fully consumed
+      for (int e = tid; e < nk * D; e += kGenThreads) {
+        int kk = e / D, d = e % D;
+        Ks[kk * (D + 1) + d] = round_to<QT>(ld(k2 + rows.k2_off(k0 + kk, g) + d));
+      }
+      for (int e = tid; e < nk * DV; e += kGenThreads) {
+        int kk = e / DV, d = e % DV;
+        V2s[kk * DV + d] = round_to<QT>(ld(v2 + rows.v2_off(k0 + kk, g) + d));
+      }
+      __syncthreads();
+      // scores (scaled) into Ps, local max
+      float lmax = -INFINITY;
+      for (int e = tid; e < nj * nk; e += kGenThreads) {
+        int jj = e / nk, kk = e % nk;
+        const float* a = As + jj * (D + 1);
+        const float* b = Ks + kk * (D + 1);
+        float s = 0.f;
+        for (int d = 0; d < D; ++d) s = fmaf(a[d], b[d], s);
+        s *= scale;
+        Ps[jj * (KB + 1) + kk] = s;
+        lmax = fmaxf(lmax, s);
+      }
+      lmax = wave_max(lmax);
+      if (lane == 0) red[wid] = lmax;
+      __syncthreads();
+      float cmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+      float mn = fmaxf(m, cmax);
+      float alpha = __expf(m - mn);
+      float lsum = 0.f;
+      for (int e = tid; e < nj * nk; e += kGenThreads) {
+        int jj = e / nk, kk = e % nk;
+        float p = __expf(Ps[jj * (KB + 1) + kk] - mn);
+        lsum += p;
+        Ps[jj * (KB + 1) + kk] = round_to<QT>(p);
+      }
+      lsum = wave_sum(lsum);
+      __syncthreads();  // everyone read red[] (max) and wrote Ps
+      if (lane == 0) red[4 + wid] = lsum;
+      __syncthreads();
+      float csum = red[4] + red[5] + red[6] + red[7];
+      z = z * alpha + csum;
+      m = mn;
+      if (tid < DV) {
+        float part = 0.f;
+        for (int jj = 0; jj < nj; ++jj) {
+          const float* prow = Ps + jj * (KB + 1);
+          float pv = 0.f;
+          for (int kk = 0; kk < nk; ++kk) pv = fmaf(prow[kk], V2s[kk * DV + tid], pv);
+          part = fmaf(pv, V1s[jj * DV + tid], part);
+        }
+        acc = acc * alpha + part;
+      }
+    }
+    __syncthreads();
+  }
+  if (tid < DV) out[tid] = (OT)(acc / z);
+  if (tid == 0 && lse) *lse = m + __logf(z);
+}
+
+}  // namespace sa

@@ -1,0 +1,36 @@
+// Host-side launch interface between the C ABI (sa_capi.hip) and the kernel
+// translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "../../include/simplicial_mi355x.h"
+
+namespace sa {
+
+struct GenericPrefillParams {
+  const void* q;
+  const void* k1;
+  const void* k2;
+  const void* v1;
+  const void* v2;
+  void* out;
+  float* lse;
+  const int32_t* cu;
+  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, lse_st;
+  int seqlen, num_seqs, group, ws, wl, d, dv;
+  float scale;
+};
+
+hipError_t launch_prefill_bf16_mfma(const sa_prefill_args* a, hipStream_t stream);
+hipError_t launch_prefill_generic(const sa_prefill_args* a, hipStream_t stream);
+
+// Paged: number of split partials per (token, head) and the launch itself.
+int paged_mfma_supported(const sa_paged_args* a);
+int paged_choose_splits(const sa_paged_args* a);
+size_t paged_workspace_bytes(const sa_paged_args* a, int splits);
+hipError_t launch_paged(const sa_paged_args* a, int splits, void* ws, size_t ws_bytes, hipStream_t stream);
+
+int device_cu_count();
+
+}  // namespace sa

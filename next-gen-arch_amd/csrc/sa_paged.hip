@@ -1,0 +1,428 @@
+// Paged-KV forward (serving form: any mix of prefill and decode tokens) for the
+// 2-simplicial attention library.  Replaces the reference's Triton _paged
+// kernel and its torch split merge (archlab/architectures/simplicial_paged.py:19-65,
+// :105-128) behind simplicial_paged_attention.
+//
+// Each query token carries (sequence, absolute position).  Its short window
+// (k1, v1) and long window (k2, v2) are gathered through one block table per
+// cache: block = table[seq, pos / block_size] (widened to int64 before the
+// stride multiply), slot = pos % block_size.
+//
+// bf16 MFMA kernel: a workgroup owns (token, KV group, split, task block).
+// A task is (query head in the group, 32-row group of the short window); NW
+// waves take NW tasks.  The long window is cut into 32-key chunks that start
+// at pos - long_window + 1; the split index partitions only the chunks that
+// hold valid keys (not the table capacity), so no split scans empty pages.
+// All waves of a workgroup consume the same chunk, double-buffered in LDS,
+// gathered with 16-byte loads (a 64-element bf16 row is 8 lanes x 16 B).
+// Every (split, row group) writes a partial (max, sum, unnormalised output);
+// sa_paged_combine merges them in a fixed order, so results are
+// run-to-run bit-identical.
+#include "sa_generic.h"
+#include "sa_mfma.h"
+#include "sa_launch.h"
+
+namespace sa {
+
+struct PagedParams {
+  const bf16* q;
+  int64_t q_st, q_sh;
+  const bf16* sc;
+  const bf16* lc;
+  int64_t sc_a, sc_b, sc_s, sc_h;
+  int64_t lc_a, lc_b, lc_s, lc_h;
+  const void* stable;
+  const void* ltable;
+  int64_t st_s, lt_s;
+  const void* tseq;
+  const void* tpos;
+  int table64, tok64;
+  int st_w, lt_w, num_seqs;
+  int64_t s_blocks, l_blocks;
+  int tokens, hq, hk, group, bs;
+  int ws, wl, nc, nr;
+  float sl2;
+  int q_neg;
+  int splits;
+  int tasks;    // group * nr
+  int tblocks;  // task blocks per (token, KV group)
+  float* part_o;  // [P][tokens][hq][D], P = splits * nr
+  float* part_m;  // [P][tokens][hq]
+  float* part_z;
+};
+
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW) void paged_mfma_kernel(PagedParams p) {
+  using L = ChunkLayout<D>;
+  constexpr int NT = 64 * NW;
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int half = lane >> 5, n = lane & 31;
+
+  int b = blockIdx.x;
+  const int tb = b % p.tblocks;
+  b /= p.tblocks;
+  const int split = b % p.splits;
+  b /= p.splits;
+  const int g = b % p.hk;
+  const int token = b / p.hk;
+
+  const int64_t seq = clamp64(load_index(p.tseq, token, p.tok64), 0, p.num_seqs - 1);
+  const int pos = (int)load_index(p.tpos, token, p.tok64);
+  const int task = tb * NW + wid;
+  const bool task_ok = task < p.tasks;
+  const int hi = task_ok ? task % p.group : 0;
+  const int r = task_ok ? task / p.group : 0;
+  const int h = g * p.group + hi;
+
+  const int lo2 = max(0, pos - p.wl + 1);
+  const int lo1 = max(0, pos - p.ws + 1);
+  const int kstart = pos - p.wl + 1;  // chunk grid origin (position)
+  const int cfirst = (lo2 - kstart) / kChunk;
+  const int nvalid = p.nc - cfirst;
+  const int per = (nvalid + p.splits - 1) / p.splits;
+  const int cbeg = cfirst + split * per;
+  const int cend = min(p.nc, cbeg + per);
+
+  auto row_off = [&](const void* table, int64_t ts, int tw, int64_t nblk, int64_t cb, int64_t cs, int64_t ch,
+                     int ps) -> int64_t {
+    const int64_t blk = block_of(table, p.table64, ts, tw, nblk, seq, ps, p.bs);
+    return blk * cb + (int64_t)(ps % p.bs) * cs + (int64_t)g * ch;
+  };
+
+  RowBlock<D> rb;
+  rb.reset();
+  const int j = pos - 32 * r - n;
+  const bool row_ok = task_ok && j >= lo1 && cbeg < cend;
+  const bf16* k1row = row_ok ? p.sc + row_off(p.stable, p.st_s, p.st_w, p.s_blocks, p.sc_b, p.sc_s, p.sc_h, j) : nullptr;
+  rb.form_a(p.q + (int64_t)token * p.q_st + (int64_t)h * p.q_sh, k1row, half, p.q_neg != 0);
+
+  auto stage = [&](ChunkStager<D, NT>& st, int c) {
+    const int k0 = kstart + kChunk * c;
+    st.load(p.lc, p.lc, tid, [&](int kk, bool is_v) -> int64_t {
+      const int ps = k0 + kk;
+      if (ps < lo2 || ps > pos) return -1;
+      const int64_t o = row_off(p.ltable, p.lt_s, p.lt_w, p.l_blocks, p.lc_b, p.lc_s, p.lc_h, ps);
+      return is_v ? o + p.lc_a : o;
+    });
+  };
+
+  if (cbeg < cend) {
+    {
+      ChunkStager<D, NT> st;
+      stage(st, cbeg);
+      st.store(lds, tid);
+    }
+    __syncthreads();
+    for (int c = cbeg; c < cend; ++c) {
+      ChunkStager<D, NT> st;
+      const bool pre = c + 1 < cend;
+      if (pre) stage(st, c + 1);
+      if (task_ok) {
+        const int kfirst = kstart + kChunk * c;
+        rb.chunk(lds + ((c - cbeg) & 1) * L::kBytes, lane, p.sl2, max(lo2 - kfirst, 0), min(pos - kfirst, kChunk - 1));
+      }
+      if (pre) st.store(lds + ((c + 1 - cbeg) & 1) * L::kBytes, tid);
+      __syncthreads();
+    }
+  }
+
+  // ---- epilogue: merge this wave's 32 rows, write one partial
+  const float zrow = rb.z + swap_halves(rb.z);
+  const float mrow = row_ok ? rb.m : -INFINITY;
+  const float Mw = wave_max(mrow);
+  const float wgt = (row_ok && Mw > -INFINITY) ? fast_exp2(mrow - Mw) : 0.f;
+  const float Zw = half_sum(wgt * zrow);
+  const bf16* v1row = row_ok ? p.sc + row_off(p.stable, p.st_s, p.st_w, p.s_blocks, p.sc_b, p.sc_s, p.sc_h, j) + p.sc_a : nullptr;
+  float* red = (float*)lds + wid * (64 * 36);
+  const int P = p.splits * p.nr;
+  const int pidx = split * p.nr + r;
+  const int64_t prow = ((int64_t)pidx * p.tokens + token) * p.hq + h;
+#pragma unroll
+  for (int sl = 0; sl < D / 64; ++sl) {
+#pragma unroll
+    for (int dbl = 0; dbl < 2; ++dbl) {
+      const int db = 2 * sl + dbl;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int dd = 32 * dbl + 8 * q4 + 4 * half;
+        bf16x4 vv = row_ok ? *(const bf16x4*)(v1row + 64 * sl + dd) : bf16x4{};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) red[(dd + e) * 36 + n] = wgt * (float)vv[e] * rb.o[db][4 * q4 + e];
+      }
+    }
+    __syncthreads();
+    float acc = 0.f;
+    const floatx4* row4 = (const floatx4*)(red + lane * 36);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      floatx4 x = row4[i];
+      acc += (x[0] + x[1]) + (x[2] + x[3]);
+    }
+    __syncthreads();
+    if (task_ok) p.part_o[prow * D + 64 * sl + lane] = acc;
+  }
+  if (task_ok && lane == 0) {
+    p.part_m[prow] = Mw;
+    p.part_z[prow] = Zw;
+  }
+  (void)P;
+}
+
+// Merge P = splits * row-groups partials per (token, head) in a fixed order.
+// One wave per (token, head); D/64 output values per lane.
+__global__ __launch_bounds__(256) void paged_combine_kernel(const float* __restrict__ part_o,
+                                                            const float* __restrict__ part_m,
+                                                            const float* __restrict__ part_z, int P, int tokens,
+                                                            int hq, int D, float* __restrict__ out, int64_t o_st,
+                                                            int64_t o_sh, float* __restrict__ lse) {
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t th = (int64_t)blockIdx.x * 4 + wid;
+  if (th >= (int64_t)tokens * hq) return;
+  const int token = (int)(th / hq), h = (int)(th % hq);
+  const int64_t stride = (int64_t)tokens * hq;
+  float M = -INFINITY;
+  for (int i = 0; i < P; ++i) M = fmaxf(M, part_m[i * stride + th]);
+  float Z = 0.f;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < P; ++i) {
+    const float mi = part_m[i * stride + th];
+    const float w = mi > -INFINITY ? fast_exp2(mi - M) : 0.f;
+    Z += w * part_z[i * stride + th];
+    const float* po = part_o + (i * stride + th) * D;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      if (64 * s < D) acc[s] += w * po[64 * s + lane];
+  }
+  const float inv = 1.f / Z;
+  float* orow = out + (int64_t)token * o_st + (int64_t)h * o_sh;
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    if (64 * s < D) orow[64 * s + lane] = acc[s] * inv;
+  if (lse && lane == 0) lse[th] = (M + __log2f(Z)) * kLn2;
+}
+
+// ---------------------------------------------------------------------------
+// Generic paged kernel: one workgroup per (token, query head), any dtype / D.
+struct GenericPagedParams {
+  const void* q;
+  int64_t q_st, q_sh;
+  PagedRows rows;
+  const void* tseq;
+  const void* tpos;
+  int tok64;
+  int num_seqs;
+  int group, ws, wl, d;
+  float scale;
+  float* out;
+  int64_t o_st, o_sh;
+  float* lse;
+  int hq;
+};
+
+template <typename QT, typename CT>
+__global__ __launch_bounds__(kGenThreads) void paged_generic_kernel(GenericPagedParams gp) {
+  const int token = blockIdx.x, h = blockIdx.y;
+  PagedRows rows = gp.rows;
+  rows.seq = clamp64(load_index(gp.tseq, token, gp.tok64), 0, gp.num_seqs - 1);
+  const int pos = (int)load_index(gp.tpos, token, gp.tok64);
+  const QT* q = (const QT*)gp.q + (int64_t)token * gp.q_st + (int64_t)h * gp.q_sh;
+  float* out = gp.out + (int64_t)token * gp.o_st + (int64_t)h * gp.o_sh;
+  float* lse = gp.lse ? gp.lse + (int64_t)token * gp.hq + h : nullptr;
+  generic_query<QT, CT, float>(q, rows, h / gp.group, pos, gp.ws, gp.wl, gp.d, gp.d, gp.scale, out, lse);
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+
+int paged_mfma_supported(const sa_paged_args* a) {
+  if (a->flags & SA_FLAG_FORCE_GENERIC) return 0;
+  if (a->q_dtype != SA_DTYPE_BF16 || a->cache_dtype != SA_DTYPE_BF16) return 0;
+  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256) return 0;
+  // 16-byte row alignment for the vector gathers
+  const int64_t* s = a->sc_stride;
+  const int64_t* l = a->lc_stride;
+  for (int i = 0; i < 4; ++i)
+    if ((s[i] % 8) || (l[i] % 8)) return 0;
+  if ((a->q_stride_t % 8) || (a->q_stride_h % 8)) return 0;
+  if (((uintptr_t)a->q | (uintptr_t)a->short_cache | (uintptr_t)a->long_cache) & 15) return 0;
+  return 1;
+}
+
+static int paged_nw(const sa_paged_args* a) {
+  const int tasks = (a->heads_q / a->heads_kv) * ((a->short_window + 31) / 32);
+  return tasks >= 4 ? 4 : (tasks >= 2 ? 2 : 1);
+}
+
+int paged_choose_splits(const sa_paged_args* a) {
+  if (!paged_mfma_supported(a)) return 1;
+  const int nc = (int)(((int64_t)a->long_window + kChunk - 1) / kChunk);
+  if (a->splits > 0) return a->splits < nc ? a->splits : nc;
+  const int group = a->heads_q / a->heads_kv;
+  const int tasks = group * ((a->short_window + 31) / 32);
+  const int nw = paged_nw(a);
+  const int64_t wgs = (int64_t)a->tokens * a->heads_kv * ((tasks + nw - 1) / nw);
+  const int64_t target = 8LL * device_cu_count();
+  int s = (int)((target + wgs - 1) / wgs);
+  if (s < 1) s = 1;
+  // at least 2 chunks per split keeps the double buffer useful
+  int cap = nc / 2 > 0 ? nc / 2 : 1;
+  if (s > cap) s = cap;
+  return s;
+}
+
+size_t paged_workspace_bytes(const sa_paged_args* a, int splits) {
+  if (!paged_mfma_supported(a)) return 0;
+  const size_t P = (size_t)splits * ((a->short_window + 31) / 32);
+  const size_t th = (size_t)a->tokens * a->heads_q;
+  size_t b = P * th * (size_t)a->head_dim * 4;
+  b = (b + 255) & ~(size_t)255;
+  size_t m = (P * th * 4 + 255) & ~(size_t)255;
+  return b + 2 * m;
+}
+
+template <int D, int NW>
+static hipError_t launch_paged_mfma_t(PagedParams p, hipStream_t stream) {
+  const size_t lds_ring = 2 * (size_t)ChunkLayout<D>::kBytes;
+  const size_t lds_red = (size_t)NW * 64 * 36 * sizeof(float);
+  const size_t lds = lds_ring > lds_red ? lds_ring : lds_red;
+  auto kern = paged_mfma_kernel<D, NW>;
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  const int64_t nb = (int64_t)p.tokens * p.hk * p.splits * p.tblocks;
+  hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(64 * NW), lds, stream, p);
+  return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_paged_mfma_d(const PagedParams& p, int nw, hipStream_t stream) {
+  if (nw == 4) return launch_paged_mfma_t<D, 4>(p, stream);
+  if (nw == 2) return launch_paged_mfma_t<D, 2>(p, stream);
+  return launch_paged_mfma_t<D, 1>(p, stream);
+}
+
+hipError_t launch_paged(const sa_paged_args* a, int splits, void* ws, size_t ws_bytes, hipStream_t stream) {
+  if (a->tokens == 0) return hipSuccess;
+  if (paged_mfma_supported(a)) {
+    PagedParams p{};
+    p.q = (const bf16*)a->q;
+    p.q_st = a->q_stride_t;
+    p.q_sh = a->q_stride_h;
+    p.sc = (const bf16*)a->short_cache;
+    p.lc = (const bf16*)a->long_cache;
+    p.sc_a = a->sc_stride[0];
+    p.sc_b = a->sc_stride[1];
+    p.sc_s = a->sc_stride[2];
+    p.sc_h = a->sc_stride[3];
+    p.lc_a = a->lc_stride[0];
+    p.lc_b = a->lc_stride[1];
+    p.lc_s = a->lc_stride[2];
+    p.lc_h = a->lc_stride[3];
+    p.stable = a->short_table;
+    p.ltable = a->long_table;
+    p.st_s = a->st_stride;
+    p.lt_s = a->lt_stride;
+    p.tseq = a->token_seq;
+    p.tpos = a->token_pos;
+    p.table64 = a->table_index_dtype == SA_INDEX_I64;
+    p.tok64 = a->token_index_dtype == SA_INDEX_I64;
+    p.st_w = a->short_table_width;
+    p.lt_w = a->long_table_width;
+    p.num_seqs = a->num_seqs;
+    p.s_blocks = a->short_blocks;
+    p.l_blocks = a->long_blocks;
+    p.tokens = a->tokens;
+    p.hq = a->heads_q;
+    p.hk = a->heads_kv;
+    p.group = a->heads_q / a->heads_kv;
+    p.bs = a->block_size;
+    p.ws = a->short_window;
+    p.wl = a->long_window;
+    p.nc = (int)(((int64_t)a->long_window + kChunk - 1) / kChunk);
+    p.nr = (a->short_window + 31) / 32;
+    p.sl2 = fabsf(a->scale) * kLog2e;
+    p.q_neg = a->scale < 0.f;
+    p.splits = splits;
+    p.tasks = p.group * p.nr;
+    const int nw = paged_nw(a);
+    p.tblocks = (p.tasks + nw - 1) / nw;
+    const size_t P = (size_t)splits * p.nr;
+    const size_t th = (size_t)a->tokens * a->heads_q;
+    char* w = (char*)ws;
+    size_t ob = (P * th * (size_t)a->head_dim * 4 + 255) & ~(size_t)255;
+    size_t mb = (P * th * 4 + 255) & ~(size_t)255;
+    if (ws_bytes < ob + 2 * mb || ((uintptr_t)ws & 255)) return hipErrorInvalidValue;
+    p.part_o = (float*)w;
+    p.part_m = (float*)(w + ob);
+    p.part_z = (float*)(w + ob + mb);
+    hipError_t e;
+    switch (a->head_dim) {
+      case 64: e = launch_paged_mfma_d<64>(p, nw, stream); break;
+      case 128: e = launch_paged_mfma_d<128>(p, nw, stream); break;
+      default: e = launch_paged_mfma_d<256>(p, nw, stream); break;
+    }
+    if (e != hipSuccess) return e;
+    const int64_t nth = (int64_t)a->tokens * a->heads_q;
+    hipLaunchKernelGGL(paged_combine_kernel, dim3((unsigned)((nth + 3) / 4)), dim3(256), 0, stream, p.part_o,
+                       p.part_m, p.part_z, (int)P, a->tokens, a->heads_q, a->head_dim, a->out, a->o_stride_t,
+                       a->o_stride_h, a->lse);
+    return hipGetLastError();
+  }
+  GenericPagedParams gp{};
+  gp.q = a->q;
+  gp.q_st = a->q_stride_t;
+  gp.q_sh = a->q_stride_h;
+  gp.rows.sc = a->short_cache;
+  gp.rows.lc = a->long_cache;
+  gp.rows.sc_a = a->sc_stride[0];
+  gp.rows.sc_b = a->sc_stride[1];
+  gp.rows.sc_s = a->sc_stride[2];
+  gp.rows.sc_h = a->sc_stride[3];
+  gp.rows.lc_a = a->lc_stride[0];
+  gp.rows.lc_b = a->lc_stride[1];
+  gp.rows.lc_s = a->lc_stride[2];
+  gp.rows.lc_h = a->lc_stride[3];
+  gp.rows.stable = a->short_table;
+  gp.rows.ltable = a->long_table;
+  gp.rows.st_s = a->st_stride;
+  gp.rows.lt_s = a->lt_stride;
+  gp.rows.table64 = a->table_index_dtype == SA_INDEX_I64;
+  gp.rows.st_w = a->short_table_width;
+  gp.rows.lt_w = a->long_table_width;
+  gp.rows.s_blocks = a->short_blocks;
+  gp.rows.l_blocks = a->long_blocks;
+  gp.rows.block_size = a->block_size;
+  gp.rows.seq = 0;
+  gp.tseq = a->token_seq;
+  gp.tpos = a->token_pos;
+  gp.tok64 = a->token_index_dtype == SA_INDEX_I64;
+  gp.num_seqs = a->num_seqs;
+  gp.group = a->heads_q / a->heads_kv;
+  gp.ws = a->short_window;
+  gp.wl = a->long_window;
+  gp.d = a->head_dim;
+  gp.scale = a->scale;
+  gp.out = a->out;
+  gp.o_st = a->o_stride_t;
+  gp.o_sh = a->o_stride_h;
+  gp.lse = a->lse;
+  gp.hq = a->heads_q;
+  const size_t lds = gen_lds_bytes(gp.d, gp.d);
+  dim3 grid(a->tokens, a->heads_q);
+  hipError_t e;
+#define SA_LAUNCH_GP(QT, CT)                                                                                 \
+  do {                                                                                                       \
+    auto kern = paged_generic_kernel<QT, CT>;                                                                \
+    e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);        \
+    if (e != hipSuccess) return e;                                                                           \
+    hipLaunchKernelGGL(kern, grid, dim3(kGenThreads), lds, stream, gp);                                      \
+  } while (0)
+  if (a->q_dtype == SA_DTYPE_F32 && a->cache_dtype == SA_DTYPE_F32) SA_LAUNCH_GP(float, float);
+  else if (a->q_dtype == SA_DTYPE_F32) SA_LAUNCH_GP(float, bf16);
+  else if (a->cache_dtype == SA_DTYPE_F32) SA_LAUNCH_GP(bf16, float);
+  else SA_LAUNCH_GP(bf16, bf16);
+#undef SA_LAUNCH_GP
+  return hipGetLastError();
+}
+
+}  // namespace sa

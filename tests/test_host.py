@@ -1,0 +1,171 @@
+"""CPU checks of the host side: the C ABI library, its Python binding, the
+reference-compatible argument contracts and the workload generators.  No
+kernel is launched here."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "simplicial_mi355x.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sa_[a-z_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from archlab_amd import _native
+    lib = _native.load()
+    declared = _declared_functions()
+    assert declared, "no declarations parsed"
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+    assert set(declared) == set(_native.EXPORTS)
+    out = subprocess.run(["nm", "-D", "--defined-only", _native.library_path()], capture_output=True, text=True)
+    exported = {line.split()[-1] for line in out.stdout.splitlines() if " T " in line}
+    assert set(declared) <= exported
+    assert lib.sa_version().startswith(b"simplicial_mi355x")
+
+
+def _c_layout(struct, fields):
+    """sizeof / offsetof of a header struct, measured by the C compiler."""
+    body = "\n".join(f'  printf("{f} %zu\\n", offsetof({struct}, {f}));' for f in fields)
+    src = f"""#include <stdio.h>
+#include <stddef.h>
+#include "simplicial_mi355x.h"
+int main(void) {{
+  printf("sizeof %zu\\n", sizeof({struct}));
+{body}
+  return 0;
+}}
+"""
+    import tempfile
+    with tempfile.TemporaryDirectory() as tmp:
+        c = os.path.join(tmp, "layout.c")
+        exe = os.path.join(tmp, "layout")
+        open(c, "w").write(src)
+        subprocess.run(["gcc", "-std=c11", "-I", os.path.dirname(HEADER), c, "-o", exe], check=True)
+        res = subprocess.run([exe], capture_output=True, text=True, check=True).stdout
+    return {k: int(v) for k, v in (line.split() for line in res.splitlines())}
+
+
+@pytest.mark.parametrize("cls,struct", [("PrefillArgs", "sa_prefill_args"), ("PagedArgs", "sa_paged_args")])
+def test_python_binding_matches_c_struct_layout(cls, struct):
+    from archlab_amd import _native
+    py = getattr(_native, cls)
+    fields = [f for f, _ in py._fields_]
+    layout = _c_layout(struct, fields)
+    assert layout["sizeof"] == ctypes.sizeof(py)
+    for f in fields:
+        assert layout[f] == getattr(py, f).offset, f
+
+
+def test_c_abi_rejects_invalid_arguments_before_any_launch():
+    from archlab_amd import _native
+    lib = _native.load()
+    args = _native.PrefillArgs(q=16, k1=16, k2=16, v1=16, v2=16, out=16, num_seqs=1, seqlen=4, total_tokens=4,
+                               heads_q=4, heads_kv=2, head_dim=64, value_dim=64, short_window=5, long_window=4,
+                               scale=1.0, dtype=_native.SA_DTYPE_BF16)
+    assert lib.sa_prefill_fwd(ctypes.byref(args), None) == _native.SA_ERR_INVALID
+    assert b"short_window" in lib.sa_last_error()
+    args.short_window, args.heads_q = 2, 3
+    assert lib.sa_prefill_fwd(ctypes.byref(args), None) == _native.SA_ERR_INVALID
+    assert b"grouped-query" in lib.sa_last_error()
+    args.heads_q, args.head_dim = 4, 48
+    assert lib.sa_prefill_fwd(ctypes.byref(args), None) == _native.SA_ERR_INVALID
+    assert lib.sa_prefill_kernel(ctypes.byref(args)) is None
+    args.head_dim = 64
+    assert lib.sa_prefill_kernel(ctypes.byref(args)) == b"mfma"
+    args.dtype = _native.SA_DTYPE_F32
+    assert lib.sa_prefill_kernel(ctypes.byref(args)) == b"generic"
+    pargs = _native.PagedArgs(tokens=1, heads_q=4, heads_kv=3, head_dim=64, block_size=16, short_window=1,
+                              long_window=2)
+    assert lib.sa_paged_fwd(ctypes.byref(pargs), None, 0, None) == _native.SA_ERR_INVALID
+    assert b"geometry" in lib.sa_last_error()
+
+
+def _cpu_inputs(b=1, n=8, hq=4, hk=2, d=64):
+    return [torch.zeros(b, n, h, d) for h in (hq, hk, hk, hk, hk)]
+
+
+def test_prefill_contract_messages_match_reference():
+    from archlab_amd import simplicial_attention
+    x = _cpu_inputs()
+    with pytest.raises(ValueError, match=r"expected \[batch, sequence, heads, head_dim\]"):
+        simplicial_attention(x[0][0], *x[1:], 2, 4)
+    with pytest.raises(ValueError, match="require 1 <= short_window <= long_window"):
+        simplicial_attention(*x, 0, 4)
+    with pytest.raises(ValueError, match="matching batch, sequence and heads"):
+        simplicial_attention(x[0], x[1][:, :4], *x[2:], 2, 4)
+    with pytest.raises(ValueError, match="incompatible grouped-query geometry"):
+        simplicial_attention(x[0][:, :, :3], *x[1:], 2, 4)
+    with pytest.raises(ValueError, match="same dtype and device"):
+        simplicial_attention(x[0].double(), *x[1:], 2, 4)
+    with pytest.raises(ValueError, match="finite real"):
+        simplicial_attention(*x, 2, 4, scale=torch.tensor(1.0))
+    with pytest.raises(ValueError, match="kernel supports CUDA float32/bfloat16"):
+        simplicial_attention(*x, 2, 4)
+
+
+def test_paged_contract_messages_match_reference():
+    from archlab_amd import simplicial_paged_attention
+    q = torch.zeros(3, 4, 64)
+    cache = torch.zeros(2, 5, 16, 2, 64)
+    table = torch.zeros(2, 3, dtype=torch.int32)
+    seq = torch.zeros(3, dtype=torch.int32)
+    kw = dict(short_window=2, long_window=4, scale=1.0)
+    with pytest.raises(ValueError, match=r"expected q \[T,H,D\]"):
+        simplicial_paged_attention(q[0], cache, cache, table, seq, seq, **kw)
+    with pytest.raises(ValueError, match="incompatible paged simplicial geometry"):
+        simplicial_paged_attention(q[:, :3], cache, cache, table, seq, seq, **kw)
+    with pytest.raises(ValueError, match="require 1 <= short_window <= long_window"):
+        simplicial_paged_attention(q, cache, cache, table, seq, seq, short_window=5, long_window=4, scale=1.0)
+    with pytest.raises(ValueError, match="invalid paged simplicial inputs"):
+        simplicial_paged_attention(q, cache, cache, table, seq, seq, **kw)  # CPU tensors
+
+
+def test_token_layout_matches_oracle():
+    from archlab_amd.serving import token_layout
+    from oracle import simplicial_oracle as O
+    starts = torch.tensor([0, 3, 4, 9, 9, 15], dtype=torch.int32)
+    lens = torch.tensor([10, 1, 7, 5, 6], dtype=torch.int32)
+    for tokens in (15, 9, 1):
+        a = token_layout(starts, lens, tokens)
+        b = O.token_layout(starts, lens, tokens)
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+        assert a[0].dtype == torch.int32 and a[1].dtype == torch.int32
+
+
+def test_workload_definitions_match_baseline():
+    from archlab_amd import workloads as W
+    from oracle import simplicial_oracle as O
+    assert W.prefill_flops(W.C2) == pytest.approx(1.0995e12, rel=1e-4)
+    assert W.prefill_flops(W.NS) == pytest.approx(2.1990e12, rel=1e-4)
+    assert W.prefill_flops(W.C4) == pytest.approx(2.1990e12, rel=1e-4)
+    assert W.prefill_flops(W.C1) == pytest.approx(2.684e8, rel=1e-3)
+    assert W.prefill_bytes(W.C2) == pytest.approx(201.9e6, rel=2e-3)
+    lengths = W.varlen_lengths(32768, 12, 1)
+    assert sum(lengths) == 32768 and len(lengths) <= 12
+    cu = W.cu_from_lengths(lengths)
+    assert cu.dtype == torch.int32 and int(cu[-1]) == 32768
+    # the valid-pair fraction quoted for C2 (93.75%) follows from causal_triples
+    full = W.C2.seqlen * W.C2.w1 * W.C2.w2
+    assert O.causal_triples(W.C2.seqlen, W.C2.w2, W.C2.w1) / full == pytest.approx(0.9375, abs=2e-3)
+
+
+def test_paged_workload_generator_small():
+    from archlab_amd import workloads as W
+    cfg = W.PagedConfig("tiny", 3, 4, 2, 64, 32, 8, 16, 20, 60, seed=3)
+    inp = W.paged_inputs(cfg)
+    t = inp["block_table"]
+    assert t.dtype == torch.int32 and t.shape == (3, 4)
+    assert int(t.min()) >= 1 and len(set(t.flatten().tolist())) == t.numel()  # distinct, null page unused
+    assert inp["short_cache"].shape == (2, 13, 16, 2, 64)
+    assert torch.equal(inp["token_pos"], (inp["ctx"] - 1).to(torch.int32))

@@ -1,0 +1,244 @@
+"""Pin the CPU oracle (oracle/simplicial_oracle.py) before trusting it.
+
+Each oracle function is checked against something that does not share its
+code: the committed brute-force fixtures, a textbook routine it reduces to,
+closed forms, invariants, or a brute-force count.  Planted-mistake tests
+show that a plausible error (dropped window bound, wrong GQA mapping,
+per-row instead of joint softmax, wrong LSE base) fails these checks.
+"""
+
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import simplicial_oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "simplicial_golden.npz")
+
+
+def _golden_cases():
+    data = np.load(GOLDEN)  # allow_pickle defaults to False
+    names = sorted({k.split("/")[0] for k in data.files})
+    out = []
+    for name in names:
+        meta = data[f"{name}/meta"].tolist()
+        tensors = {k: torch.from_numpy(data[f"{name}/{k}"]) for k in ("q", "k1", "k2", "v1", "v2", "out", "lse")}
+        out.append((name, meta, tensors))
+    return out
+
+
+def _inputs(b=1, n=6, hq=4, hk=2, d=4, seed=42, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, n, hq, d, generator=g, dtype=dtype)
+    return [q] + [torch.randn(b, n, hk, d, generator=g, dtype=dtype) for _ in range(4)]
+
+
+@pytest.mark.parametrize("case", _golden_cases(), ids=lambda c: c[0])
+def test_oracle_matches_brute_force_fixtures(case):
+    name, (b, n, hq, hk, d, ws, wl, seed), t = case
+    out, lse = O.reference_simplicial(t["q"], t["k1"], t["k2"], t["v1"], t["v2"], ws, wl,
+                                      scale=d ** -0.5, return_lse=True)
+    torch.testing.assert_close(out, t["out"], rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(lse, t["lse"], rtol=1e-12, atol=1e-12)
+
+
+def test_single_pair_is_value_product():
+    x = _inputs()
+    out = O.reference_simplicial(*x, 1, 1)
+    torch.testing.assert_close(out, (x[3] * x[4]).repeat_interleave(2, dim=2))
+
+
+def test_ones_reduce_to_local_softmax_attention():
+    """k1 = v1 = 1: the score no longer depends on j, so the joint softmax is
+    ordinary causal sliding-window attention on (q, k2, v2) -- a textbook
+    routine (SDPA with a band mask)."""
+    g = torch.Generator().manual_seed(3)
+    b, n, h, d, ws, wl = 1, 23, 2, 8, 4, 7
+    q, k2, v2 = (torch.randn(b, n, h, d, generator=g, dtype=torch.float64) for _ in range(3))
+    ones = torch.ones(b, n, h, d, dtype=torch.float64)
+    scale = 0.1
+    out = O.reference_simplicial(q, ones, k2, ones, v2, ws, wl, scale=scale)
+    i = torch.arange(n)[:, None]
+    k = torch.arange(n)[None, :]
+    band = (k <= i) & (k > i - wl)
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        q.transpose(1, 2), k2.transpose(1, 2), v2.transpose(1, 2), attn_mask=band, scale=scale).transpose(1, 2)
+    torch.testing.assert_close(out, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_both_key_axes_are_causal():
+    x = _inputs(n=8)
+    expected = O.reference_simplicial(*x, 3, 5)[:, :4]
+    for branch in range(1, 5):
+        altered = [t.clone() for t in x]
+        altered[branch][:, 4:] += 100
+        torch.testing.assert_close(O.reference_simplicial(*altered, 3, 5)[:, :4], expected)
+
+
+def test_windows_exclude_keys_older_than_the_window():
+    x = _inputs(n=10)
+    ws, wl, i = 3, 5, 9
+    base = O.reference_simplicial(*x, ws, wl, query_positions=[i])
+    alt = [t.clone() for t in x]
+    alt[1][:, : i - ws + 1] += 50  # k1 rows outside the short window
+    alt[2][:, : i - wl + 1] += 50  # k2 rows outside the long window
+    torch.testing.assert_close(O.reference_simplicial(*alt, ws, wl, query_positions=[i]), base)
+    alt[2][:, i - wl + 1] += 50  # the oldest row inside the long window does matter
+    assert not torch.allclose(O.reference_simplicial(*alt, ws, wl, query_positions=[i]), base)
+
+
+def test_joint_softmax_is_not_per_row():
+    """Planted mistake: normalising each j row separately differs from the oracle."""
+    x = _inputs(n=5, hq=2, hk=2)
+    q, k1, k2, v1, v2 = x
+    i, ws, wl = 4, 2, 3
+    out = O.reference_simplicial(*x, ws, wl, query_positions=[i])[:, 0]
+    j = slice(i - ws + 1, i + 1)
+    k = slice(i - wl + 1, i + 1)
+    s = torch.einsum("bhd,bjhd,bkhd->bhjk", q[:, i], k1[:, j], k2[:, k]) / 2
+    per_row = torch.einsum("bhjk,bjhd,bkhd->bhd", s.softmax(-1) / ws, v1[:, j], v2[:, k])
+    assert not torch.allclose(per_row, out, atol=1e-6)
+
+
+def test_gqa_uses_contiguous_head_groups():
+    """Query head h reads KV head h // G; a planted h % HK mapping differs."""
+    x = _inputs(n=7, hq=6, hk=2)
+    out = O.reference_simplicial(*x, 2, 4)
+    for h in range(6):
+        kv = h // 3
+        single = O.reference_simplicial(x[0][:, :, h:h + 1], *(t[:, :, kv:kv + 1] for t in x[1:]), 2, 4)
+        torch.testing.assert_close(out[:, :, h:h + 1], single)
+    wrong = O.reference_simplicial(x[0][:, :, 1:2], *(t[:, :, 1:2] for t in x[1:]), 2, 4)  # h=1 -> kv 1
+    assert not torch.allclose(out[:, :, 1:2], wrong)
+
+
+def test_lse_is_natural_log_and_merges_exactly():
+    x = _inputs(n=9)
+    ws, wl = 3, 6
+    out, lse = O.reference_simplicial(*x, ws, wl, return_lse=True)
+    # closed form: log sum exp over valid pairs, natural log (not log2)
+    q, k1, k2 = x[0], x[1].repeat_interleave(2, 2), x[2].repeat_interleave(2, 2)
+    i = 7
+    s = torch.einsum("bhd,bjhd,bkhd->bhjk", q[:, i], k1[:, i - ws + 1:i + 1], k2[:, i - wl + 1:i + 1]) / 2
+    torch.testing.assert_close(lse[:, i], torch.log(torch.exp(s).sum((-1, -2))), rtol=1e-12, atol=1e-12)
+    assert not torch.allclose(lse[:, i], torch.log2(torch.exp(s).sum((-1, -2))))
+    # any partition of the long window merges back through the LSE weights
+    v1, v2 = x[3].repeat_interleave(2, 2), x[4].repeat_interleave(2, 2)
+    parts = []
+    for lo, hi in ((i - wl + 1, i - 2), (i - 2, i + 1)):
+        sp = torch.einsum("bhd,bjhd,bkhd->bhjk", q[:, i], k1[:, i - ws + 1:i + 1], k2[:, lo:hi]) / 2
+        m = torch.logsumexp(sp.flatten(-2), -1)
+        o = torch.einsum("bhjk,bjhd,bkhd->bhd", torch.exp(sp - m[..., None, None]), v1[:, i - ws + 1:i + 1], v2[:, lo:hi])
+        parts.append((m, o))
+    top = torch.maximum(parts[0][0], parts[1][0])
+    w = [torch.exp(m - top) for m, _ in parts]
+    merged = (w[0][..., None] * parts[0][1] + w[1][..., None] * parts[1][1]) / (w[0] + w[1])[..., None]
+    torch.testing.assert_close(merged, out[:, i], rtol=1e-12, atol=1e-12)
+
+
+def test_varlen_is_per_sequence_dense():
+    g = torch.Generator().manual_seed(5)
+    lengths = [5, 1, 9]
+    t = sum(lengths)
+    q = torch.randn(t, 4, 8, generator=g, dtype=torch.float64)
+    k1, k2, v1, v2 = (torch.randn(t, 2, 8, generator=g, dtype=torch.float64) for _ in range(4))
+    cu = torch.tensor([0, 5, 6, 15], dtype=torch.int32)
+    out, lse = O.varlen_reference(q, k1, k2, v1, v2, cu, 2, 4, return_lse=True)
+    for s in range(3):
+        lo, hi = int(cu[s]), int(cu[s + 1])
+        o, l = O.reference_simplicial(*(x[None, lo:hi] for x in (q, k1, k2, v1, v2)), 2, 4, return_lse=True)
+        torch.testing.assert_close(out[lo:hi], o[0], rtol=0, atol=0)
+        torch.testing.assert_close(lse[lo:hi], l[0], rtol=0, atol=0)
+    # planted: attending across the document boundary changes the second document
+    glued = O.reference_simplicial(*(x[None] for x in (q, k1, k2, v1, v2)), 2, 4)[0]
+    assert not torch.allclose(glued[6:8], out[6:8])
+    sub = O.varlen_reference(q, k1, k2, v1, v2, cu, 2, 4, query_positions=[14, 0, 5])
+    torch.testing.assert_close(sub, out[[0, 5, 14]], rtol=0, atol=0)
+
+
+def _paged_fixture(lengths, hk, d, block_size, seed, dtype=torch.float64, hnd=False):
+    """Contiguous K/V per sequence plus the same rows scattered into shuffled pages."""
+    g = torch.Generator().manual_seed(seed)
+    per = [math.ceil(n / block_size) for n in lengths]
+    total = 1 + sum(per)
+    perm = (torch.randperm(total - 1, generator=g) + 1).tolist()
+    table = torch.zeros(len(lengths), max(per), dtype=torch.int32)
+    shape = (2, total, hk, block_size, d) if hnd else (2, total, block_size, hk, d)
+    caches = [torch.zeros(shape, dtype=dtype) for _ in range(2)]
+    dense = []
+    for s, n in enumerate(lengths):
+        table[s, :per[s]] = torch.tensor(perm[:per[s]], dtype=torch.int32)
+        perm = perm[per[s]:]
+        k1, k2, v1, v2 = (torch.randn(n, hk, d, generator=g, dtype=dtype) for _ in range(4))
+        dense.append((k1, k2, v1, v2))
+        for p in range(n):
+            blk, off = int(table[s, p // block_size]), p % block_size
+            for cache, (k, v) in zip(caches, ((k1, v1), (k2, v2))):
+                view = cache.transpose(2, 3) if hnd else cache
+                view[0, blk, off] = k[p]
+                view[1, blk, off] = v[p]
+    if hnd:
+        caches = [c.transpose(2, 3) for c in caches]
+    return caches, table, dense
+
+
+@pytest.mark.parametrize("hnd", [False, True])
+def test_paged_reference_equals_dense_on_gathered_rows(hnd):
+    lengths, hq, hk, d, bs = [1, 23, 40], 4, 2, 8, 16
+    (short, long), table, dense = _paged_fixture(lengths, hk, d, bs, seed=3, hnd=hnd)
+    g = torch.Generator().manual_seed(9)
+    seqs, poss, qs, exp_o, exp_l = [], [], [], [], []
+    for s, n in enumerate(lengths):
+        q = torch.randn(1, n, hq, d, generator=g, dtype=torch.float64)
+        k1, k2, v1, v2 = dense[s]
+        o, l = O.reference_simplicial(q, k1[None], k2[None], v1[None], v2[None], 4, 16, scale=0.3,
+                                      return_lse=True)
+        for p in (range(n) if s != 1 else [n - 1]):
+            seqs.append(s), poss.append(p), qs.append(q[0, p]), exp_o.append(o[0, p]), exp_l.append(l[0, p])
+    out, lse = O.paged_reference(torch.stack(qs), short, long, table, torch.tensor(seqs), torch.tensor(poss),
+                                 short_window=4, long_window=16, scale=0.3, return_lse=True)
+    torch.testing.assert_close(out, torch.stack(exp_o), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(lse, torch.stack(exp_l), rtol=1e-12, atol=1e-12)
+
+
+def test_paged_gather_addressing_is_table_driven():
+    (short, _), table, dense = _paged_fixture([30], 1, 4, 8, seed=1)
+    k, v = O.paged_gather(short, table, 0, list(range(30)))
+    torch.testing.assert_close(k, dense[0][0], rtol=0, atol=0)
+    torch.testing.assert_close(v, dense[0][2], rtol=0, atol=0)
+    # planted: indexing blocks without the table returns different rows
+    wrong = short[0, 1 + torch.arange(30) // 8, torch.arange(30) % 8]
+    assert not torch.equal(wrong, dense[0][0])
+
+
+def test_token_layout_matches_brute_force():
+    starts = torch.tensor([0, 3, 4, 9, 9])
+    lens = torch.tensor([10, 1, 7, 5])
+    seq, pos = O.token_layout(starts, lens, 9)
+    exp_seq, exp_pos = [], []
+    for s in range(4):
+        n = int(starts[s + 1] - starts[s])
+        for k in range(n):
+            exp_seq.append(s)
+            exp_pos.append(int(lens[s]) - n + k)
+    assert seq.tolist() == exp_seq and pos.tolist() == exp_pos
+
+
+@pytest.mark.parametrize("length,short,long", [(1, 1, 1), (7, 2, 3), (40, 5, 33), (100, 32, 512), (600, 32, 512)])
+def test_causal_triples_matches_brute_force(length, short, long):
+    brute = sum(min(i + 1, short) * min(i + 1, long) for i in range(length))
+    assert O.causal_triples(length, short, long) == brute
+    brute_pairs = sum(min(i + 1, long) for i in range(length))
+    assert O.causal_pairs(length, long) == brute_pairs
+
+
+def test_scale_contract():
+    assert O._score_scale(None, 64) == pytest.approx(1 / 8)
+    assert O._score_scale(2, 64) == 2.0
+    with pytest.raises(ValueError):
+        O._score_scale(float("inf"), 64)
+    with pytest.raises(ValueError):
+        O._score_scale(torch.tensor(1.0), 64)

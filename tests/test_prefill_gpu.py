@@ -1,0 +1,199 @@
+"""GPU parity of the prefill kernels (dense and packed varlen) against the CPU oracle.
+
+Inputs are seeded; the oracle receives exactly the values the kernel sees
+(bf16 inputs upcast to fp32).  Tolerances: bf16 out max-abs <= 2e-2 and LSE
+relative <= 1e-3; fp32 <= 1e-4.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_lse_close, assert_out_close, rand_inputs
+from oracle import simplicial_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "simplicial_golden.npz")
+
+
+def _api():
+    from archlab_amd.architectures.simplicial_attention import (
+        prefill_kernel_name, simplicial_attention, simplicial_varlen_attention)
+    return simplicial_attention, simplicial_varlen_attention, prefill_kernel_name
+
+
+def _check(cuda, b, n, hq, hk, d, ws, wl, dtype, seed=0, positions=None, scale=1.0, sigma=1.0, kernel="auto"):
+    attn, _, name = _api()
+    x = rand_inputs(b, n, hq, hk, d, seed=seed, dtype=dtype, sigma=sigma)
+    out, lse = attn(*(t.to(cuda) for t in x), ws, wl, scale=scale, return_lse=True, kernel=kernel)
+    torch.cuda.synchronize()
+    ref_o, ref_l = O.reference_simplicial(*(t.float() for t in x), ws, wl, scale=scale,
+                                          query_positions=positions, return_lse=True)
+    if positions is not None:
+        out, lse = out[:, positions], lse[:, positions]
+    e1 = assert_out_close(out, ref_o, dtype)
+    e2 = assert_lse_close(lse, ref_l, dtype)
+    print(f"[{name(x[0], x[1], x[3], kernel=kernel)}] b{b} n{n} h{hq}/{hk} d{d} w{ws}x{wl} {dtype}: "
+          f"out {e1:.2e} lse {e2:.2e}", flush=True)
+    return out, lse
+
+
+def test_golden_fixtures_fp32(cuda):
+    attn, _, _ = _api()
+    data = np.load(GOLDEN)
+    names = sorted({k.split("/")[0] for k in data.files})
+    for nm in names:
+        b, n, hq, hk, d, ws, wl, seed = data[f"{nm}/meta"].tolist()
+        x = [torch.from_numpy(data[f"{nm}/{k}"]).float().to(cuda) for k in ("q", "k1", "k2", "v1", "v2")]
+        out, lse = attn(*x, ws, wl, return_lse=True)
+        torch.testing.assert_close(out.cpu().double(), torch.from_numpy(data[f"{nm}/out"]), rtol=1e-4, atol=1e-4)
+        torch.testing.assert_close(lse.cpu().double(), torch.from_numpy(data[f"{nm}/lse"]), rtol=1e-4, atol=1e-4)
+
+
+def test_c1_fp32_full(cuda):
+    """B1 H4 S512 D64, w1=32 (long), w2=16 (short), fp32, seed 0."""
+    _check(cuda, 1, 512, 4, 4, 64, 16, 32, torch.float32, seed=0)
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("hq,hk", [(4, 4), (4, 2), (8, 2), (3, 1)])
+def test_mfma_small_windows(cuda, d, hq, hk):
+    _check(cuda, 2, 150, hq, hk, d, 16, 64, torch.bfloat16, seed=d + hq, kernel="mfma")
+
+
+@pytest.mark.parametrize("ws,wl", [(1, 1), (5, 33), (32, 32), (33, 100), (64, 256), (100, 130), (32, 10_000)])
+def test_mfma_window_edges(cuda, ws, wl):
+    _check(cuda, 1, 300, 4, 2, 128, ws, wl, torch.bfloat16, seed=ws * 7 + wl, kernel="mfma")
+
+
+def test_mfma_production_windows(cuda):
+    """Reference production geometry: short 32, long 512, GQA 4, positions across both edges."""
+    pos = [0, 1, 30, 31, 32, 33, 100, 510, 511, 512, 513, 700, 1023, 1100, 1199]
+    _check(cuda, 1, 1200, 8, 2, 128, 32, 512, torch.bfloat16, seed=5, positions=pos, kernel="mfma")
+
+
+def test_mfma_scale_variants(cuda):
+    _check(cuda, 1, 200, 4, 4, 64, 8, 40, torch.bfloat16, seed=3, scale=None, kernel="mfma")
+    _check(cuda, 1, 200, 4, 4, 64, 8, 40, torch.bfloat16, seed=3, scale=-0.7, kernel="mfma")
+    _check(cuda, 1, 200, 4, 4, 64, 8, 40, torch.bfloat16, seed=3, scale=0.0, kernel="mfma")
+
+
+def test_generic_bf16_and_fp32(cuda):
+    _check(cuda, 1, 100, 4, 2, 128, 16, 40, torch.bfloat16, seed=1, kernel="generic")
+    _check(cuda, 1, 100, 4, 2, 32, 16, 40, torch.float32, seed=2, kernel="generic")
+    _check(cuda, 1, 70, 2, 1, 512, 8, 20, torch.float32, seed=4)
+    _check(cuda, 1, 70, 2, 2, 16, 3, 9, torch.bfloat16, seed=6)
+
+
+def test_value_dim_differs(cuda):
+    attn, _, _ = _api()
+    x = rand_inputs(1, 60, 4, 2, 64, dv=32, seed=8, dtype=torch.float32)
+    out = attn(*(t.to(cuda) for t in x), 4, 20)
+    ref = O.reference_simplicial(*x, 4, 20)
+    assert_out_close(out, ref, torch.float32)
+
+
+def test_mfma_matches_generic(cuda):
+    attn, _, _ = _api()
+    x = [t.to(cuda) for t in rand_inputs(2, 400, 8, 2, 128, seed=11)]
+    a, la = attn(*x, 32, 128, scale=1.0, return_lse=True, kernel="mfma")
+    b, lb = attn(*x, 32, 128, scale=1.0, return_lse=True, kernel="generic")
+    assert (a.float() - b.float()).abs().max().item() < 1e-2
+    assert (la - lb).abs().max().item() < 1e-3
+
+
+@pytest.mark.parametrize("seed", [0])
+def test_c2_full_size_sampled(cuda, seed):
+    """BASELINE config 2 at full size (B2 H16 S4096 D128, 512x32), window-edge positions."""
+    pos = [0, 31, 32, 511, 512, 1000, 2047, 4095]
+    _check(cuda, 2, 4096, 16, 16, 128, 32, 512, torch.bfloat16, seed=seed, positions=pos, kernel="mfma")
+
+
+def test_d256_config4_sampled_and_deterministic(cuda):
+    """BASELINE config 4 shape family (D=256, w1=256, w2=64, sigma 0.5), shortened; bit-exact reruns."""
+    attn, _, _ = _api()
+    pos = [0, 63, 64, 255, 256, 1000, 2047]
+    out, lse = _check(cuda, 1, 2048, 8, 8, 256, 64, 256, torch.bfloat16, seed=4, sigma=0.5,
+                      positions=pos, kernel="mfma")
+    x = [t.to(cuda) for t in rand_inputs(1, 2048, 8, 8, 256, seed=4, sigma=0.5)]
+    runs = [attn(*x, 64, 256, scale=1.0, return_lse=True) for _ in range(3)]
+    for o, l in runs[1:]:
+        assert torch.equal(o, runs[0][0]) and torch.equal(l, runs[0][1])
+
+
+def test_deterministic_algorithms_allowed(cuda):
+    attn, _, _ = _api()
+    x = [t.to(cuda) for t in rand_inputs(1, 64, 2, 2, 64, seed=1)]
+    prev = torch.are_deterministic_algorithms_enabled()
+    torch.use_deterministic_algorithms(True)
+    try:
+        a = attn(*x, 4, 16)
+        b = attn(*x, 4, 16)
+    finally:
+        torch.use_deterministic_algorithms(prev)
+    assert torch.equal(a, b)
+
+
+def test_noncontiguous_inputs(cuda):
+    attn, _, _ = _api()
+    x = [t.to(cuda) for t in rand_inputs(1, 96, 4, 2, 64, seed=9)]
+    base = attn(*x, 8, 40)
+    strided = [t.transpose(1, 2).contiguous().transpose(1, 2) for t in x]
+    assert not strided[0].is_contiguous()
+    assert torch.equal(attn(*strided, 8, 40), base)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_varlen_matches_per_sequence(cuda, dtype):
+    attn, varlen, _ = _api()
+    lengths = [1, 37, 300, 5, 129]
+    t = sum(lengths)
+    x = rand_inputs(1, t, 8, 2, 128 if dtype == torch.bfloat16 else 64, seed=21, dtype=dtype)
+    packed = [v[0].to(cuda) for v in x]
+    cu = torch.tensor([0] + list(np.cumsum(lengths)), dtype=torch.int32, device=cuda)
+    out, lse = varlen(*packed, cu, 16, 64, scale=1.0, return_lse=True)
+    start = 0
+    for n in lengths:
+        sl = slice(start, start + n)
+        o, l = attn(*(p[None, sl] for p in packed), 16, 64, scale=1.0, return_lse=True)
+        assert torch.equal(out[sl], o[0]), "varlen differs from the per-sequence dense call"
+        assert torch.equal(lse[sl], l[0])
+        start += n
+    ref_o, ref_l = O.varlen_reference(*(v[0].float() for v in x), cu.cpu(), 16, 64, scale=1.0, return_lse=True)
+    assert_out_close(out, ref_o, dtype)
+    assert_lse_close(lse, ref_l, dtype)
+
+
+def test_c3_varlen_gqa_sampled(cuda):
+    """BASELINE config 3 (T=32768 packed, 12 sequences, HQ32/HKV8, D128, 512x32) at sampled tokens."""
+    from archlab_amd.workloads import C3, prefill_inputs
+    _, varlen, _ = _api()
+    q, k1, k2, v1, v2, cu = prefill_inputs(C3)
+    out, lse = varlen(*(t.to(cuda) for t in (q, k1, k2, v1, v2)), cu.to(cuda), C3.w2, C3.w1, scale=1.0,
+                      return_lse=True)
+    cu_l = cu.tolist()
+    pos = sorted({c for c in cu_l[:-1]} | {c + 31 for c in cu_l[:3]} | {c + 600 for c in cu_l[:4]} | {32767})
+    ref_o, ref_l = O.varlen_reference(*(t.float() for t in (q, k1, k2, v1, v2)), cu, C3.w2, C3.w1, scale=1.0,
+                                      query_positions=pos, return_lse=True)
+    assert_out_close(out[pos], ref_o, torch.bfloat16)
+    assert_lse_close(lse[pos], ref_l, torch.bfloat16)
+
+
+def test_contract_errors(cuda):
+    attn, varlen, _ = _api()
+    x = [t.to(cuda) for t in rand_inputs(1, 8, 4, 2, 64)]
+    with pytest.raises(ValueError, match="short_window <= long_window"):
+        attn(*x, 5, 4)
+    with pytest.raises(ValueError, match="grouped-query"):
+        attn(x[0][:, :, :3], *x[1:], 2, 4)
+    with pytest.raises(ValueError, match="CUDA float32/bfloat16"):
+        attn(*(t.half() for t in x), 2, 4)
+    with pytest.raises(ValueError, match="finite real"):
+        attn(*x, 2, 4, scale=float("nan"))
+    with pytest.raises(ValueError, match="forward-only"):
+        attn(x[0].float().requires_grad_(), *(t.float() for t in x[1:]), 2, 4)
+    with pytest.raises(ValueError, match="MFMA kernel does not cover"):
+        attn(*(t.float() for t in x), 2, 4, kernel="mfma")
