@@ -22,7 +22,7 @@ from .simplicial_attention import _kernel_flag
 
 
 def _paged_args(q, short_cache, long_cache, block_table, long_block_table, token_seq, token_pos,
-                short_window, long_window, scale, splits, out, lse, flags):
+                short_window, long_window, scale, splits, out, lse, flags, plan_only=False):
     tokens, heads, dim = q.shape
     return _native.PagedArgs(
         q=q.data_ptr(), q_stride_t=q.stride(0), q_stride_h=q.stride(1),
@@ -31,7 +31,7 @@ def _paged_args(q, short_cache, long_cache, block_table, long_block_table, token
         short_table=block_table.data_ptr(), st_stride=block_table.stride(0),
         long_table=long_block_table.data_ptr(), lt_stride=long_block_table.stride(0),
         token_seq=token_seq.data_ptr(), token_pos=token_pos.data_ptr(),
-        out=out.data_ptr() if out is not None else None,
+        out=out.data_ptr() if out is not None else (256 if plan_only else None),
         o_stride_t=out.stride(0) if out is not None else heads * dim,
         o_stride_h=out.stride(1) if out is not None else dim,
         lse=lse.data_ptr() if lse is not None else None,
@@ -121,7 +121,7 @@ def paged_plan(q, short_cache, long_cache, block_table, token_seq, token_pos, *,
     long_block_table = block_table if long_block_table is None else long_block_table
     lib = _native.load()
     args = _paged_args(q, short_cache, long_cache, block_table, long_block_table, token_seq, token_pos,
-                       short_window, long_window, scale, splits, None, None, _kernel_flag(kernel))
+                       short_window, long_window, scale, splits, None, None, _kernel_flag(kernel), plan_only=True)
     name = lib.sa_paged_kernel(ctypes.byref(args))
     return (None if name is None else name.decode(), lib.sa_paged_splits(ctypes.byref(args)),
             lib.sa_paged_workspace_bytes(ctypes.byref(args)))

@@ -56,10 +56,20 @@ __device__ __forceinline__ floatx16 mfma32x32x16(const bf16x8& a, const bf16x8& 
 // register r by lane l:  row_of(r, l) = 8*(r/4) + 4*(l/32) + r%4.
 __device__ __forceinline__ int acc_row(int r, int half) { return 8 * (r >> 2) + 4 * half + (r & 3); }
 
-// Exchange a 32-bit value with the lane 32 positions away (l <-> l ^ 32).
-__device__ __forceinline__ float swap_halves(float x) {
+// Reductions across the two 32-lane halves of a wave with v_permlane32_swap.
+// With both operands = x, the instruction returns two registers that hold,
+// in EVERY lane l, the pair {x[l % 32], x[l % 32 + 32]} (one register keeps
+// the lane's own half, the other receives the opposite half).  Combining the
+// two registers therefore gives the same two-half result in all 64 lanes, in
+// the same operand order (bit-identical halves).
+__device__ __forceinline__ float pair_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float pair_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // xor-shuffle within groups of 32 lanes (ds_swizzle bit-mask mode, no
@@ -87,15 +97,9 @@ __device__ __forceinline__ float half_sum(float x) {
   return x + swz_xor<1>(x);
 }
 
-__device__ __forceinline__ float wave_max(float x) {
-  x = half_max(x);
-  return fmaxf(x, swap_halves(x));
-}
+__device__ __forceinline__ float wave_max(float x) { return pair_max(half_max(x)); }
 
-__device__ __forceinline__ float wave_sum(float x) {
-  x = half_sum(x);
-  return x + swap_halves(x);
-}
+__device__ __forceinline__ float wave_sum(float x) { return pair_sum(half_sum(x)); }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -51,12 +51,18 @@ struct PagedParams {
   float* part_z;
 };
 
-template <int D, int NW>
-__global__ __launch_bounds__(64 * NW) void paged_mfma_kernel(PagedParams p) {
-  using L = ChunkLayout<D>;
-  constexpr int NT = 64 * NW;
+constexpr int kPageCache = 256;  // page ids of one split kept in LDS
+
+template <int D, int NW, int P>
+__global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel(PagedParams p) {
+  using T = Tile<D>;
+  constexpr int ROWS = kChunk;
+  constexpr int SLOT = 2 * ROWS * T::kRowBytes;
+  constexpr int R = P + 1;
+  constexpr int NI = 2 * ROWS / T::kRowsPerDma / NW;  // DMA instructions per wave per tile
   extern __shared__ __attribute__((aligned(16))) char lds[];
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, n = lane & 31;
 
   int b = blockIdx.x;
@@ -67,8 +73,10 @@ __global__ __launch_bounds__(64 * NW) void paged_mfma_kernel(PagedParams p) {
   const int g = b % p.hk;
   const int token = b / p.hk;
 
-  const int64_t seq = clamp64(load_index(p.tseq, token, p.tok64), 0, p.num_seqs - 1);
-  const int pos = (int)load_index(p.tpos, token, p.tok64);
+  // per-token scalars (metadata loads are uniform: keep them in SGPRs)
+  const int64_t seq = clamp64(__builtin_amdgcn_readfirstlane((int)load_index(p.tseq, token, p.tok64)), 0,
+                              p.num_seqs - 1);
+  const int pos = __builtin_amdgcn_readfirstlane((int)load_index(p.tpos, token, p.tok64));
   const int task = tb * NW + wid;
   const bool task_ok = task < p.tasks;
   const int hi = task_ok ? task % p.group : 0;
@@ -97,45 +105,63 @@ __global__ __launch_bounds__(64 * NW) void paged_mfma_kernel(PagedParams p) {
   const bf16* k1row = row_ok ? p.sc + row_off(p.stable, p.st_s, p.st_w, p.s_blocks, p.sc_b, p.sc_s, p.sc_h, j) : nullptr;
   rb.form_a(p.q + (int64_t)token * p.q_st + (int64_t)h * p.q_sh, k1row, half, p.q_neg != 0);
 
-  auto stage = [&](ChunkStager<D, NT>& st, int c) {
+  // The page ids of this split's long-window rows are staged in LDS first:
+  // a block-table load inside the pipeline would be a vector load whose
+  // result feeds a DMA address, and waiting for it would also wait for every
+  // older tile load (vector loads complete in order).
+  int64_t* pcache = (int64_t*)(lds + R * SLOT);
+  const int ps_lo = max(lo2, kstart + kChunk * cbeg);
+  const int ps_hi = min(pos, kstart + kChunk * cend - 1);
+  const int page_lo = ps_lo / p.bs;
+  const int npages = ps_hi / p.bs - page_lo + 1;
+  const bool cached = cbeg < cend && npages <= kPageCache;
+  if (cached) {
+    for (int i = tid; i < npages; i += 64 * NW)
+      pcache[i] = block_of(p.ltable, p.table64, p.lt_s, p.lt_w, p.l_blocks, seq, (page_lo + i) * p.bs, p.bs);
+    __syncthreads();
+  }
+
+  // tile rows outside [lo2, pos] re-read the nearest valid row (masked later)
+  auto issue = [&](int c) {
     const int k0 = kstart + kChunk * c;
-    st.load(p.lc, p.lc, tid, [&](int kk, bool is_v) -> int64_t {
-      const int ps = k0 + kk;
-      if (ps < lo2 || ps > pos) return -1;
-      const int64_t o = row_off(p.ltable, p.lt_s, p.lt_w, p.l_blocks, p.lc_b, p.lc_s, p.lc_h, ps);
-      return is_v ? o + p.lc_a : o;
+    issue_tile<D, ROWS, NW>(lds + (c % R) * SLOT, p.lc, p.lc + p.lc_a, wid, lane, [&](int row, bool) -> int64_t {
+      const int ps = min(max(k0 + row, lo2), pos);
+      const int pg = ps / p.bs;
+      const int64_t blk = cached ? pcache[pg - page_lo]
+                                 : block_of(p.ltable, p.table64, p.lt_s, p.lt_w, p.l_blocks, seq, ps, p.bs);
+      return blk * p.lc_b + (int64_t)(ps - pg * p.bs) * p.lc_s + (int64_t)g * p.lc_h;
     });
   };
 
   if (cbeg < cend) {
-    {
-      ChunkStager<D, NT> st;
-      stage(st, cbeg);
-      st.store(lds, tid);
-    }
-    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < P; ++e)
+      if (cbeg + e < cend) issue(cbeg + e);
     for (int c = cbeg; c < cend; ++c) {
-      ChunkStager<D, NT> st;
-      const bool pre = c + 1 < cend;
-      if (pre) stage(st, c + 1);
+      const int ahead = min(P - 1, cend - 1 - c);
+      if constexpr (P >= 4) { if (ahead >= 3) wait_vmcnt<3 * NI>(); else if (ahead == 2) wait_vmcnt<2 * NI>(); else if (ahead == 1) wait_vmcnt<NI>(); else wait_vmcnt<0>(); }
+      else if constexpr (P == 3) { if (ahead >= 2) wait_vmcnt<2 * NI>(); else if (ahead == 1) wait_vmcnt<NI>(); else wait_vmcnt<0>(); }
+      else if constexpr (P == 2) { if (ahead >= 1) wait_vmcnt<NI>(); else wait_vmcnt<0>(); }
+      else { wait_vmcnt<0>(); }
+      block_barrier();
+      if (c + P < cend) issue(c + P);
       if (task_ok) {
         const int kfirst = kstart + kChunk * c;
-        rb.chunk(lds + ((c - cbeg) & 1) * L::kBytes, lane, p.sl2, max(lo2 - kfirst, 0), min(pos - kfirst, kChunk - 1));
+        const char* slot = lds + (c % R) * SLOT;
+        rb.chunk(slot, slot + ROWS * T::kRowBytes, 0, lane, p.sl2, max(lo2 - kfirst, 0), min(pos - kfirst, kChunk - 1));
       }
-      if (pre) st.store(lds + ((c + 1 - cbeg) & 1) * L::kBytes, tid);
-      __syncthreads();
     }
+    block_barrier();
   }
 
   // ---- epilogue: merge this wave's 32 rows, write one partial
-  const float zrow = rb.z + swap_halves(rb.z);
+  const float zrow = pair_sum(rb.z);
   const float mrow = row_ok ? rb.m : -INFINITY;
   const float Mw = wave_max(mrow);
   const float wgt = (row_ok && Mw > -INFINITY) ? fast_exp2(mrow - Mw) : 0.f;
   const float Zw = half_sum(wgt * zrow);
   const bf16* v1row = row_ok ? p.sc + row_off(p.stable, p.st_s, p.st_w, p.s_blocks, p.sc_b, p.sc_s, p.sc_h, j) + p.sc_a : nullptr;
   float* red = (float*)lds + wid * (64 * 36);
-  const int P = p.splits * p.nr;
   const int pidx = split * p.nr + r;
   const int64_t prow = ((int64_t)pidx * p.tokens + token) * p.hq + h;
 #pragma unroll
@@ -151,7 +177,7 @@ __global__ __launch_bounds__(64 * NW) void paged_mfma_kernel(PagedParams p) {
         for (int e = 0; e < 4; ++e) red[(dd + e) * 36 + n] = wgt * (float)vv[e] * rb.o[db][4 * q4 + e];
       }
     }
-    __syncthreads();
+    block_barrier();
     float acc = 0.f;
     const floatx4* row4 = (const floatx4*)(red + lane * 36);
 #pragma unroll
@@ -159,14 +185,13 @@ __global__ __launch_bounds__(64 * NW) void paged_mfma_kernel(PagedParams p) {
       floatx4 x = row4[i];
       acc += (x[0] + x[1]) + (x[2] + x[3]);
     }
-    __syncthreads();
+    block_barrier();
     if (task_ok) p.part_o[prow * D + 64 * sl + lane] = acc;
   }
   if (task_ok && lane == 0) {
     p.part_m[prow] = Mw;
     p.part_z[prow] = Zw;
   }
-  (void)P;
 }
 
 // Merge P = splits * row-groups partials per (token, head) in a fixed order.
@@ -281,12 +306,15 @@ size_t paged_workspace_bytes(const sa_paged_args* a, int splits) {
   return b + 2 * m;
 }
 
+constexpr int kPagedDepth = 3;  // tiles in flight per workgroup
+
 template <int D, int NW>
 static hipError_t launch_paged_mfma_t(PagedParams p, hipStream_t stream) {
-  const size_t lds_ring = 2 * (size_t)ChunkLayout<D>::kBytes;
+  constexpr int P = D >= 256 ? 2 : kPagedDepth;
+  const size_t lds_ring = (size_t)(P + 1) * 2 * kChunk * Tile<D>::kRowBytes + kPageCache * sizeof(int64_t);
   const size_t lds_red = (size_t)NW * 64 * 36 * sizeof(float);
   const size_t lds = lds_ring > lds_red ? lds_ring : lds_red;
-  auto kern = paged_mfma_kernel<D, NW>;
+  auto kern = paged_mfma_kernel<D, NW, P>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   const int64_t nb = (int64_t)p.tokens * p.hk * p.splits * p.tblocks;

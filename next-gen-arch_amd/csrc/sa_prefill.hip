@@ -5,19 +5,21 @@
 //
 // bf16 MFMA kernel (D in {64, 128, 256}, DV == D)
 // ------------------------------------------------
-// A workgroup of 4 waves owns NQ query tokens spaced 32 apart
-// (t_w = base + 32*w), NH query heads of one KV group and NRG short-axis row
-// groups, NQ*NH*NRG == 4.  Each wave handles one (token, head, row group):
-// 32 A rows a_j = bf16(q_t ⊙ k1_j).  All queries of the block walk the long
-// window in 32-key chunks that start at t - long_window + 1, so a query's
-// window is covered by exactly ceil(long_window / 32) chunks and tokens spaced
-// 32 apart share the same chunk grid: wave w uses block chunk (c + qw) in
-// iteration c.  Chunks stream through an LDS ring of NQ + 1 slots, one chunk
-// prefetched per iteration, one barrier per iteration.
+// A workgroup of 4 waves owns NQ consecutive query tokens t0 .. t0+NQ-1 and
+// NH query heads of one KV group (NQ * NH == 4).  Wave w handles token
+// t0 + w / NH, head w % NH: its 32 A rows a_j = bf16(q_t ⊙ k1_j).  Every query
+// walks its long window in 32-key chunks that start at t - long_window + 1,
+// so ceil(long_window / 32) chunks cover it exactly.  Chunk c of the NQ
+// queries together spans 32 + NQ - 1 keys; that K/V tile is loaded once per
+// step and wave w reads it from row w / NH.  Tiles stream through an LDS
+// ring of P + 1 slots by direct global->LDS DMA, P tiles ahead of use, one
+// barrier per step.
 //
 // The joint softmax is kept per A row (running max / sum); the epilogue merges
 // the rows with their log-sum-exp weights and applies v1:
 //     out = sum_j w_j (v1_j ⊙ O_j) / sum_j w_j z_j,   w_j = exp(m_j - max m).
+// Short windows longer than 32 are processed in passes of 32 rows whose
+// results are merged the same way.
 #include "sa_generic.h"
 #include "sa_mfma.h"
 #include "sa_launch.h"
@@ -58,10 +60,9 @@ __device__ __forceinline__ int seq_start(const int32_t* cu, int num_seqs, int se
     if (cu[mid] <= t) lo = mid;
     else hi = mid - 1;
   }
-  return min(max(cu[lo], 0), t);
+  // uniform across the wave (every lane searched the same t): keep it scalar
+  return __builtin_amdgcn_readfirstlane(min(max(cu[lo], 0), t));
 }
-
-__device__ __forceinline__ int seq_start_of(const PrefillParams& p, int t) { return seq_start(p.cu, p.num_seqs, p.seqlen, t); }
 
 // Workgroups are dispatched round-robin over the 8 XCDs; remap so that each
 // XCD (own L2) walks a contiguous range of logical blocks (neighbouring
@@ -72,108 +73,121 @@ __device__ __forceinline__ int xcd_remap(int b, int n) {
   return x * q + min(x, r) + i;
 }
 
-template <int D, int NQ, int NH, int NRG>
-__global__ __launch_bounds__(256, 1) void prefill_mfma_kernel(PrefillParams p) {
-  static_assert(NQ * NH * NRG == 4, "4 waves per block");
-  using L = ChunkLayout<D>;
-  constexpr int R = NQ + 1;  // ring slots
+// Wait until at most k later tiles (NI DMA instructions each) are in flight.
+template <int NI, int P>
+__device__ __forceinline__ void wait_tiles(int k) {
+  if constexpr (P >= 4) {
+    if (k >= 3) { wait_vmcnt<NI * 3>(); return; }
+  }
+  if constexpr (P >= 3) {
+    if (k >= 2) { wait_vmcnt<NI * 2>(); return; }
+  }
+  if constexpr (P >= 2) {
+    if (k >= 1) { wait_vmcnt<NI>(); return; }
+  }
+  wait_vmcnt<0>();
+}
+
+template <int D, int NQ, int NH, int P>
+__global__ __launch_bounds__(256, (D >= 256 ? 1 : 2)) void prefill_mfma_kernel(PrefillParams p) {
+  static_assert(NQ * NH == 4, "4 waves per block");
+  static_assert(P >= 1 && P <= 4, "prefetch depth");
+  using T = Tile<D>;
+  constexpr int NW = 4;
+  constexpr int ROWS = tile_rows<D>(kChunk + NQ - 1, NW);
+  constexpr int SLOT = 2 * ROWS * T::kRowBytes;
+  constexpr int R = P + 1;
+  constexpr int NI = 2 * ROWS / T::kRowsPerDma / NW;  // DMA instructions per wave per tile
   extern __shared__ __attribute__((aligned(16))) char lds[];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wid = tid >> 6;
-  const int rg = wid % NRG;
-  const int hw = (wid / NRG) % NH;
-  const int qw = wid / (NRG * NH);
+  const int lane = tid & 63;
+  // wave index as a uniform (scalar) value: everything derived from it stays
+  // in SGPRs and the control flow below stays scalar
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hw = wid % NH, qo = wid / NH;
 
   const int lb = xcd_remap(blockIdx.x, p.nblocks);
   const int qb = lb % p.qblocks;
   const int hg = lb / p.qblocks;  // = g * hsub + hs
   const int g = hg / p.hsub, hs = hg % p.hsub;
-  const int base = (qb / 32) * (32 * NQ) + (qb % 32);
-  if (base >= p.total) return;
+  const int t0 = qb * NQ;
+  if (t0 >= p.total) return;
 
-  const int t = base + 32 * qw;
+  // per-wave scalars (readfirstlane pins them to SGPRs)
+  const int t = __builtin_amdgcn_readfirstlane(t0 + qo);
   const bool qvalid = t < p.total;
-  const int h = g * p.group + hs * NH + hw;
-  const int s0 = qvalid ? seq_start_of(p, t) : 0;
-  const int lo2 = max(s0, t - p.wl + 1);
-  const int lo1 = max(s0, t - p.ws + 1);
-  // first chunk with a valid key, for this wave and for the block
-  const int cfirst = qvalid ? (lo2 - (t - p.wl + 1)) / kChunk : p.nc;
-  int c0 = p.nc;
+  const int h = __builtin_amdgcn_readfirstlane(g * p.group + hs * NH + hw);
+  const int s0 = qvalid ? seq_start(p.cu, p.num_seqs, p.seqlen, t) : 0;
+  const int lo2 = __builtin_amdgcn_readfirstlane(max(s0, t - p.wl + 1));
+  const int lo1 = __builtin_amdgcn_readfirstlane(max(s0, t - p.ws + 1));
+  const int cfirst = __builtin_amdgcn_readfirstlane(qvalid ? (lo2 - (t - p.wl + 1)) / kChunk : p.nc);
+  int c0 = p.nc;  // first step in which any query of the block has a valid key
 #pragma unroll
   for (int w = 0; w < NQ; ++w) {
-    const int tw = base + 32 * w;
+    const int tw = t0 + w;
     if (tw < p.total) {
-      const int sw = seq_start_of(p, tw);
-      const int l2 = max(sw, tw - p.wl + 1);
-      c0 = min(c0, (l2 - (tw - p.wl + 1)) / kChunk);
+      const int sw = seq_start(p.cu, p.num_seqs, p.seqlen, tw);
+      c0 = min(c0, (max(sw, tw - p.wl + 1) - (tw - p.wl + 1)) / kChunk);
     }
   }
+  c0 = __builtin_amdgcn_readfirstlane(c0);
 
-  const int kbase0 = base - p.wl + 1;  // first key of block chunk 0
-  const int total = p.total;
-  const int64_t k_st = p.k_st, k_sh = p.k_sh, v_st = p.v_st, v_sh = p.v_sh;
-  auto stage = [&](ChunkStager<D, 256>& st, int e) {
-    const int k0 = kbase0 + kChunk * e;
-    st.load(p.k2, p.v2, tid, [&](int kk, bool is_v) -> int64_t {
-      const int key = k0 + kk;
-      if (key < 0 || key >= total) return -1;
-      return is_v ? (int64_t)key * v_st + (int64_t)g * v_sh : (int64_t)key * k_st + (int64_t)g * k_sh;
+  const int kb0 = t0 - p.wl + 1;  // key of tile row 0 at chunk 0
+  const int last = p.total - 1;
+  const int64_t k_st = p.k_st, v_st = p.v_st;
+  const int64_t k_g = (int64_t)g * p.k_sh, v_g = (int64_t)g * p.v_sh;
+  auto issue = [&](int c) {
+    const int key0 = kb0 + kChunk * c;
+    issue_tile<D, ROWS, NW>(lds + (c % R) * SLOT, p.k2, p.v2, wid, lane, [&](int row, bool is_v) -> int64_t {
+      const int key = min(max(key0 + row, 0), last);
+      return is_v ? (int64_t)key * v_st + v_g : (int64_t)key * k_st + k_g;
     });
   };
 
   const int half = lane >> 5, n = lane & 31;
   RowBlock<D> rb;
-  // Running merge over this wave's row-group passes: out slice values for
-  // d = 64*i + lane, plus (M, Z) in the log2 domain.
+  // Running merge over the row-group passes: out values for d = 64*i + lane,
+  // plus (M, Z) in the log2 domain.
   float orun[D / 64];
 #pragma unroll
   for (int i = 0; i < D / 64; ++i) orun[i] = 0.f;
   float Mrun = -INFINITY, Zrun = 0.f;
 
-  const int npass = (p.nr + NRG - 1) / NRG;
-  for (int ps = 0; ps < npass; ++ps) {
-    const int r = ps * NRG + rg;
+  for (int r = 0; r < p.nr; ++r) {
     const int j = t - 32 * r - n;  // this lane's short-axis key
-    const bool row_ok = qvalid && r < p.nr && j >= lo1;
+    const bool row_ok = qvalid && j >= lo1;
     rb.reset();
     rb.form_a(p.q + (int64_t)t * p.q_st + (int64_t)h * p.q_sh,
-              row_ok ? p.k1 + (int64_t)j * k_st + (int64_t)g * k_sh : nullptr, half, p.q_neg != 0);
+              row_ok ? p.k1 + (int64_t)j * k_st + k_g : nullptr, half, p.q_neg != 0);
 
-    // ---- ring prologue: chunks c0 .. c0+NQ-1
-    {
-      ChunkStager<D, 256> st;
-#pragma unroll 1
-      for (int e = 0; e < NQ; ++e) {
-        stage(st, c0 + e);
-        st.store(lds + ((c0 + e) % R) * L::kBytes, tid);
-      }
-    }
-    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < P; ++e)
+      if (c0 + e < p.nc) issue(c0 + e);
     for (int c = c0; c < p.nc; ++c) {
-      ChunkStager<D, 256> st;
-      const int enext = c + NQ;
-      const bool pre = enext <= p.nc - 1 + NQ - 1;
-      if (pre) stage(st, enext);
+      wait_tiles<NI, P>(min(P - 1, p.nc - 1 - c));
+      block_barrier();  // tile c complete for every wave; slot of tile c-1 free
+      if (c + P < p.nc) issue(c + P);
       if (qvalid && c >= cfirst) {
-        const int kfirst = t - p.wl + 1 + kChunk * c;  // key of chunk row 0
-        const int klo = max(lo2 - kfirst, 0);
-        const int khi = min(t - kfirst, kChunk - 1);
-        rb.chunk(lds + ((c + qw) % R) * L::kBytes, lane, p.sl2, klo, khi);
+        const int kfirst = t - p.wl + 1 + kChunk * c;  // key of this wave's chunk row 0
+        const char* slot = lds + (c % R) * SLOT;
+        rb.chunk(slot, slot + ROWS * T::kRowBytes, qo, lane, p.sl2, max(lo2 - kfirst, 0),
+                 min(t - kfirst, kChunk - 1));
       }
-      if (pre) st.store(lds + (enext % R) * L::kBytes, tid);
-      __syncthreads();
     }
+    block_barrier();  // ring reads done: LDS reused below
 
     // ---- epilogue of this pass: merge the 32 rows of the wave
-    const float zrow = rb.z + swap_halves(rb.z);
+    const float zrow = pair_sum(rb.z);
     const float mrow = row_ok ? rb.m : -INFINITY;
     const float Mw = wave_max(mrow);
     const float wgt = (row_ok && Mw > -INFINITY) ? fast_exp2(mrow - Mw) : 0.f;
     const float Zw = half_sum(wgt * zrow);
     float* red = (float*)lds + wid * (64 * 36);  // [64 d][36] per wave
-    const bf16* v1row = p.v1 + (int64_t)(row_ok ? j : 0) * v_st + (int64_t)g * v_sh;
+    const bf16* v1row = p.v1 + (int64_t)(row_ok ? j : 0) * v_st + v_g;
+    const float Mn = fmaxf(Mrun, Mw);
+    const float a0 = Mrun > -INFINITY ? fast_exp2(Mrun - Mn) : 0.f;
+    const float a1 = Mw > -INFINITY ? fast_exp2(Mw - Mn) : 0.f;
 #pragma unroll
     for (int sl = 0; sl < D / 64; ++sl) {
 #pragma unroll
@@ -187,7 +201,7 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_kernel(PrefillParams p) {
           for (int e = 0; e < 4; ++e) red[(dd + e) * 36 + n] = wgt * (float)vv[e] * rb.o[db][4 * q4 + e];
         }
       }
-      __syncthreads();
+      block_barrier();
       float acc = 0.f;
       const floatx4* row4 = (const floatx4*)(red + lane * 36);
 #pragma unroll
@@ -195,51 +209,14 @@ __global__ __launch_bounds__(256, 1) void prefill_mfma_kernel(PrefillParams p) {
         floatx4 x = row4[i];
         acc += (x[0] + x[1]) + (x[2] + x[3]);
       }
-      __syncthreads();
-      // merge into the running result of this wave
-      const float Mn = fmaxf(Mrun, Mw);
-      const float a0 = Mrun > -INFINITY ? fast_exp2(Mrun - Mn) : 0.f;
-      const float a1 = Mw > -INFINITY ? fast_exp2(Mw - Mn) : 0.f;
+      block_barrier();
       orun[sl] = orun[sl] * a0 + acc * a1;
     }
-    {
-      const float Mn = fmaxf(Mrun, Mw);
-      const float a0 = Mrun > -INFINITY ? fast_exp2(Mrun - Mn) : 0.f;
-      const float a1 = Mw > -INFINITY ? fast_exp2(Mw - Mn) : 0.f;
-      Zrun = Zrun * a0 + Zw * a1;
-      Mrun = Mn;
-    }
+    Zrun = Zrun * a0 + Zw * a1;
+    Mrun = Mn;
   }
 
-  // ---- merge the NRG waves of the same (token, head) and write out / lse
-  if constexpr (NRG > 1) {
-    float* part = (float*)lds + wid * (D + 2);
-#pragma unroll
-    for (int i = 0; i < D / 64; ++i) part[64 * i + lane] = orun[i];
-    if (lane == 0) {
-      part[D] = Mrun;
-      part[D + 1] = Zrun;
-    }
-    __syncthreads();
-    if (rg == 0) {
-      float M = -INFINITY;
-#pragma unroll
-      for (int k = 0; k < NRG; ++k) M = fmaxf(M, ((float*)lds + (wid + k) * (D + 2))[D]);
-      float Z = 0.f;
-      for (int i = 0; i < D / 64; ++i) orun[i] = 0.f;
-#pragma unroll
-      for (int k = 0; k < NRG; ++k) {
-        const float* pk = (float*)lds + (wid + k) * (D + 2);
-        const float wk = pk[D] > -INFINITY ? fast_exp2(pk[D] - M) : 0.f;
-        Z += wk * pk[D + 1];
-#pragma unroll
-        for (int i = 0; i < D / 64; ++i) orun[i] += wk * pk[64 * i + lane];
-      }
-      Mrun = M;
-      Zrun = Z;
-    }
-  }
-  if (rg == 0 && qvalid) {
+  if (qvalid) {
     const float inv = 1.f / Zrun;
     bf16* orow = p.out + (int64_t)t * p.o_st + (int64_t)h * p.o_sh;
 #pragma unroll
@@ -266,38 +243,37 @@ __global__ __launch_bounds__(kGenThreads) void prefill_generic_kernel(GenericPre
 // ---------------------------------------------------------------------------
 // Host launchers
 
-template <int D, int NQ, int NH, int NRG>
+template <int D, int NQ, int NH, int P>
 static hipError_t launch_prefill_mfma(const PrefillParams& base_p, hipStream_t stream) {
   PrefillParams p = base_p;
-  const int span = 32 * NQ;
-  p.qblocks = ((p.total + span - 1) / span) * 32;
+  p.qblocks = (p.total + NQ - 1) / NQ;
   p.hsub = p.group / NH;
   p.nblocks = p.qblocks * p.hk * p.hsub;
-  constexpr int R = NQ + 1;
-  size_t lds = (size_t)R * ChunkLayout<D>::kBytes;
+  constexpr int ROWS = tile_rows<D>(kChunk + NQ - 1, 4);
+  size_t lds = (size_t)(P + 1) * 2 * ROWS * Tile<D>::kRowBytes;
   const size_t red = (size_t)4 * 64 * 36 * sizeof(float);
   if (lds < red) lds = red;
-  auto kern = prefill_mfma_kernel<D, NQ, NH, NRG>;
+  auto kern = prefill_mfma_kernel<D, NQ, NH, P>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(p.nblocks), dim3(256), lds, stream, p);
   return hipGetLastError();
 }
 
+// Prefetch depth per configuration: the ring is sized to leave room for two
+// workgroups per CU (<= 80 KB) where registers allow it.
 template <int D>
 static hipError_t dispatch_prefill_mfma_d(const PrefillParams& p, hipStream_t stream) {
   const int G = p.group;
-  const bool multi_rg = p.nr >= 2;
-  if (G % 4 == 0) {
-    return launch_prefill_mfma<D, 1, 4, 1>(p, stream);
+  if constexpr (D >= 256) {
+    if (G % 4 == 0) return launch_prefill_mfma<D, 1, 4, 2>(p, stream);
+    if (G % 2 == 0) return launch_prefill_mfma<D, 2, 2, 2>(p, stream);
+    return launch_prefill_mfma<D, 4, 1, 2>(p, stream);
+  } else {
+    if (G % 4 == 0) return launch_prefill_mfma<D, 1, 4, 4>(p, stream);
+    if (G % 2 == 0) return launch_prefill_mfma<D, 2, 2, 3>(p, stream);
+    return launch_prefill_mfma<D, 4, 1, 3>(p, stream);
   }
-  if (G % 2 == 0) {
-    if (multi_rg) return launch_prefill_mfma<D, 1, 2, 2>(p, stream);
-    return launch_prefill_mfma<D, 2, 2, 1>(p, stream);
-  }
-  if (multi_rg) return launch_prefill_mfma<D, 2, 1, 2>(p, stream);
-  if (D >= 256) return launch_prefill_mfma<D, 2, 1, 2>(p, stream);
-  return launch_prefill_mfma<D, 4, 1, 1>(p, stream);
 }
 
 hipError_t launch_prefill_bf16_mfma(const sa_prefill_args* a, hipStream_t stream) {

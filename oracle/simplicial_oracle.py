@@ -81,6 +81,36 @@ def reference_simplicial(q, k1, k2, v1, v2, short_window, long_window, *,
     return out
 
 
+def kernel_rounding_reference(q, k1, k2, v1, v2, short_window, long_window, *, query_positions=None,
+                              scale=None, round_to=torch.bfloat16):
+    """The oracle with the reference KERNEL's rounding point applied.
+
+    simplicial_kernels.py:35 forms ``a = (q * k1)`` in fp32 and rounds it to
+    the input dtype before the score dot.  This evaluates the same math as
+    ``reference_simplicial`` but with every a_j = round_to(q_i ⊙ k1_j), in
+    float64 otherwise.  Returns (O, LSE).  With ``round_to=None`` it is
+    ``reference_simplicial`` in float64.
+    """
+    scale = _score_scale(scale, q.shape[-1])
+    groups = q.shape[2] // k1.shape[2]
+    k1, k2, v1, v2 = [x.double().repeat_interleave(groups, dim=2) for x in (k1, k2, v1, v2)]
+    q = q.double()
+    outs, lses = [], []
+    positions = range(q.shape[1]) if query_positions is None else query_positions
+    for i in positions:
+        j = slice(max(0, i - short_window + 1), i + 1)
+        k = slice(max(0, i - long_window + 1), i + 1)
+        a = q[:, i][:, None] * k1[:, j]  # [B, J, H, D]
+        if round_to is not None:
+            a = a.float().to(round_to).double()
+        scores = torch.einsum("bjhd,bkhd->bhjk", a, k2[:, k]) * scale
+        flat = scores.flatten(-2)
+        p = flat.softmax(-1).reshape_as(scores)
+        outs.append(torch.einsum("bhjk,bjhd,bkhd->bhd", p, v1[:, j], v2[:, k]))
+        lses.append(torch.logsumexp(flat, -1))
+    return torch.stack(outs, dim=1), torch.stack(lses, dim=1)
+
+
 def varlen_reference(q, k1, k2, v1, v2, cu_seqlens, short_window, long_window, *,
                      scale=None, return_lse=False, query_positions=None):
     """Packed variable-length form: q [T,HQ,D], keys [T,HK,D], cu_seqlens [nseq+1].

@@ -29,6 +29,9 @@ CASES = [
     ("single_pair", 1, 6, 2, 2, 4, 1, 1, 5),
     ("equal_windows", 1, 12, 2, 1, 8, 4, 4, 9),
     ("global_long", 1, 21, 2, 2, 8, 3, 10_000, 13),
+    # head dims the GPU kernels accept (16..512)
+    ("gqa_d32", 1, 24, 4, 2, 32, 4, 9, 17),
+    ("mha_d16_long", 2, 19, 2, 2, 16, 2, 10_000, 19),
 ]
 
 

@@ -242,3 +242,22 @@ def test_scale_contract():
         O._score_scale(float("inf"), 64)
     with pytest.raises(ValueError):
         O._score_scale(torch.tensor(1.0), 64)
+
+
+def test_kernel_rounding_reference_pinned():
+    """Without rounding it is the oracle; when q ⊙ k1 is exactly representable
+    in bf16 (small integers) the rounding is the identity; otherwise it
+    differs from the unrounded oracle by O(bf16 ulp)."""
+    x = _inputs(n=10)
+    o, l = O.reference_simplicial(*x, 3, 6, return_lse=True)
+    o2, l2 = O.kernel_rounding_reference(*x, 3, 6, round_to=None)
+    torch.testing.assert_close(o2, o, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(l2, l, rtol=1e-12, atol=1e-12)
+    g = torch.Generator().manual_seed(2)
+    ints = [torch.randint(-3, 4, t.shape, generator=g).double() for t in x]
+    o, l = O.reference_simplicial(*ints, 3, 6, return_lse=True, scale=0.05)
+    o3, l3 = O.kernel_rounding_reference(*ints, 3, 6, scale=0.05)
+    torch.testing.assert_close(o3, o, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(l3, l, rtol=1e-12, atol=1e-12)
+    o4, l4 = O.kernel_rounding_reference(*x, 3, 6)
+    assert 0 < (l4 - l2).abs().max() < 0.05

@@ -25,19 +25,50 @@ def _api():
     return simplicial_attention, simplicial_varlen_attention, prefill_kernel_name
 
 
-def _check(cuda, b, n, hq, hk, d, ws, wl, dtype, seed=0, positions=None, scale=1.0, sigma=1.0, kernel="auto"):
+def _check(cuda, b, n, hq, hk, d, ws, wl, dtype, seed=0, positions=None, scale=1.0, sigma=1.0, kernel="auto",
+           dv=None):
+    """Kernel vs oracle on seeded inputs; returns (out, lse) at ``positions``.
+
+    bf16 criteria (all printed before asserting):
+      * out vs the fp32 oracle: max-abs <= 2e-2 (+ half a bf16 ulp of |ref|);
+      * lse vs the fp32 oracle: rel <= 1e-3 at positions whose windows hold
+        >= 64 (j, k) pairs, rel <= 1e-2 everywhere -- with a handful of pairs
+        the LSE carries the bf16 rounding of a = q ⊙ k1 that the reference
+        kernel applies (simplicial_kernels.py:35) undiluted;
+      * vs the oracle with that same rounding point (kernel_rounding_reference):
+        lse rel <= 1e-4 and out <= 4e-3 (+ one bf16 ulp) at every position.
+    """
     attn, _, name = _api()
-    x = rand_inputs(b, n, hq, hk, d, seed=seed, dtype=dtype, sigma=sigma)
+    x = rand_inputs(b, n, hq, hk, d, dv=dv, seed=seed, dtype=dtype, sigma=sigma)
     out, lse = attn(*(t.to(cuda) for t in x), ws, wl, scale=scale, return_lse=True, kernel=kernel)
     torch.cuda.synchronize()
+    pos = list(range(n)) if positions is None else list(positions)
     ref_o, ref_l = O.reference_simplicial(*(t.float() for t in x), ws, wl, scale=scale,
-                                          query_positions=positions, return_lse=True)
-    if positions is not None:
-        out, lse = out[:, positions], lse[:, positions]
-    e1 = assert_out_close(out, ref_o, dtype)
-    e2 = assert_lse_close(lse, ref_l, dtype)
-    print(f"[{name(x[0], x[1], x[3], kernel=kernel)}] b{b} n{n} h{hq}/{hk} d{d} w{ws}x{wl} {dtype}: "
-          f"out {e1:.2e} lse {e2:.2e}", flush=True)
+                                          query_positions=pos, return_lse=True)
+    out, lse = out[:, pos].cpu(), lse[:, pos].cpu()
+    label = f"[{name(x[0], x[1], x[3], kernel=kernel)}] b{b} n{n} h{hq}/{hk} d{d} w{ws}x{wl} {dtype}"
+    if dtype != torch.bfloat16:
+        e1 = assert_out_close(out, ref_o, dtype)
+        e2 = assert_lse_close(lse, ref_l, dtype)
+        print(f"{label}: out {e1:.2e} lse {e2:.2e}", flush=True)
+        return out, lse
+    full = [i for i, p in enumerate(pos) if min(p + 1, ws) * min(p + 1, wl) >= 64]
+    ro, rl = O.kernel_rounding_reference(*x, ws, wl, scale=scale, query_positions=pos)
+    rel = lambda a, e: ((a.float() - e.float()).abs() / e.float().abs().clamp_min(1.0)).max().item()  # noqa: E731
+    stats = {
+        "out": (out.float() - ref_o).abs().max().item(),
+        "lse_full": rel(lse[:, full], ref_l[:, full]) if full else 0.0,
+        "lse_all": rel(lse, ref_l),
+        "r_out": (out.float() - ro.float()).abs().max().item(),
+        "r_lse": rel(lse, rl),
+    }
+    print(label + ": " + " ".join(f"{k} {v:.2e}" for k, v in stats.items()), flush=True)
+    assert_out_close(out, ref_o, dtype)
+    if full:
+        assert_lse_close(lse[:, full], ref_l[:, full], dtype)
+    assert_lse_close(lse, ref_l, dtype, rtol=1e-2)
+    assert_out_close(out, ro, dtype, atol=4e-3, rtol=2.0 ** -7)
+    assert_lse_close(lse, rl, dtype, rtol=1e-4)
     return out, lse
 
 
@@ -45,12 +76,17 @@ def test_golden_fixtures_fp32(cuda):
     attn, _, _ = _api()
     data = np.load(GOLDEN)
     names = sorted({k.split("/")[0] for k in data.files})
+    ran = 0
     for nm in names:
         b, n, hq, hk, d, ws, wl, seed = data[f"{nm}/meta"].tolist()
+        if d < 16:  # the kernels accept score head dims 16..512 (reference contract)
+            continue
+        ran += 1
         x = [torch.from_numpy(data[f"{nm}/{k}"]).float().to(cuda) for k in ("q", "k1", "k2", "v1", "v2")]
         out, lse = attn(*x, ws, wl, return_lse=True)
         torch.testing.assert_close(out.cpu().double(), torch.from_numpy(data[f"{nm}/out"]), rtol=1e-4, atol=1e-4)
         torch.testing.assert_close(lse.cpu().double(), torch.from_numpy(data[f"{nm}/lse"]), rtol=1e-4, atol=1e-4)
+    assert ran >= 3
 
 
 def test_c1_fp32_full(cuda):
@@ -84,7 +120,7 @@ def test_mfma_scale_variants(cuda):
 def test_generic_bf16_and_fp32(cuda):
     _check(cuda, 1, 100, 4, 2, 128, 16, 40, torch.bfloat16, seed=1, kernel="generic")
     _check(cuda, 1, 100, 4, 2, 32, 16, 40, torch.float32, seed=2, kernel="generic")
-    _check(cuda, 1, 70, 2, 1, 512, 8, 20, torch.float32, seed=4)
+    _check(cuda, 1, 70, 2, 1, 512, 8, 20, torch.float32, seed=4, dv=64)
     _check(cuda, 1, 70, 2, 2, 16, 3, 9, torch.bfloat16, seed=6)
 
 
@@ -101,7 +137,7 @@ def test_mfma_matches_generic(cuda):
     x = [t.to(cuda) for t in rand_inputs(2, 400, 8, 2, 128, seed=11)]
     a, la = attn(*x, 32, 128, scale=1.0, return_lse=True, kernel="mfma")
     b, lb = attn(*x, 32, 128, scale=1.0, return_lse=True, kernel="generic")
-    assert (a.float() - b.float()).abs().max().item() < 1e-2
+    assert_out_close(a, b, torch.bfloat16, atol=1e-2, rtol=2.0 ** -7)
     assert (la - lb).abs().max().item() < 1e-3
 
 
@@ -116,8 +152,7 @@ def test_d256_config4_sampled_and_deterministic(cuda):
     """BASELINE config 4 shape family (D=256, w1=256, w2=64, sigma 0.5), shortened; bit-exact reruns."""
     attn, _, _ = _api()
     pos = [0, 63, 64, 255, 256, 1000, 2047]
-    out, lse = _check(cuda, 1, 2048, 8, 8, 256, 64, 256, torch.bfloat16, seed=4, sigma=0.5,
-                      positions=pos, kernel="mfma")
+    _check(cuda, 1, 2048, 8, 8, 256, 64, 256, torch.bfloat16, seed=4, sigma=0.5, positions=pos, kernel="mfma")
     x = [t.to(cuda) for t in rand_inputs(1, 2048, 8, 8, 256, seed=4, sigma=0.5)]
     runs = [attn(*x, 64, 256, scale=1.0, return_lse=True) for _ in range(3)]
     for o, l in runs[1:]:
@@ -164,7 +199,11 @@ def test_varlen_matches_per_sequence(cuda, dtype):
         start += n
     ref_o, ref_l = O.varlen_reference(*(v[0].float() for v in x), cu.cpu(), 16, 64, scale=1.0, return_lse=True)
     assert_out_close(out, ref_o, dtype)
-    assert_lse_close(lse, ref_l, dtype)
+    starts = np.repeat(np.cumsum([0] + lengths[:-1]), lengths)
+    local = np.arange(t) - starts + 1
+    full = torch.from_numpy(np.minimum(local, 16) * np.minimum(local, 64) >= 64)
+    assert_lse_close(lse[full], ref_l[full], dtype)
+    assert_lse_close(lse, ref_l, dtype, rtol=1e-2)
 
 
 def test_c3_varlen_gqa_sampled(cuda):
@@ -175,11 +214,14 @@ def test_c3_varlen_gqa_sampled(cuda):
     out, lse = varlen(*(t.to(cuda) for t in (q, k1, k2, v1, v2)), cu.to(cuda), C3.w2, C3.w1, scale=1.0,
                       return_lse=True)
     cu_l = cu.tolist()
-    pos = sorted({c for c in cu_l[:-1]} | {c + 31 for c in cu_l[:3]} | {c + 600 for c in cu_l[:4]} | {32767})
+    pos = sorted({c for c in cu_l[:-1]} | {c + 31 for c in cu_l[:3]} | {c + 200 for c in cu_l[:4]} | {32767})
     ref_o, ref_l = O.varlen_reference(*(t.float() for t in (q, k1, k2, v1, v2)), cu, C3.w2, C3.w1, scale=1.0,
                                       query_positions=pos, return_lse=True)
     assert_out_close(out[pos], ref_o, torch.bfloat16)
-    assert_lse_close(lse[pos], ref_l, torch.bfloat16)
+    starts = {c for c in cu_l[:-1]}
+    full = [i for i, p in enumerate(pos) if p not in starts]  # every sampled non-start token has >= 31 rows
+    assert_lse_close(lse[pos][full], ref_l[full], torch.bfloat16)
+    assert_lse_close(lse[pos], ref_l, torch.bfloat16, rtol=1e-2)
 
 
 def test_contract_errors(cuda):
