@@ -130,6 +130,18 @@ def decode_leg(args):
     return res
 
 
+def copy_leg(args):
+    """Plain device copy of a known byte count (1 GiB read + 1 GiB written per
+    call): the calibration kernel for the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+    n = 1 << 29  # bf16 elements = 1 GiB
+    src = torch.ones(n, dtype=torch.bfloat16, device="cuda:0")
+    dst = torch.empty_like(src)
+    mean_ms, _, _ = _time_kernel(lambda: dst.copy_(src), max(2, args.steps // 4), 1)
+    return {"bytes_read": 2 * n, "bytes_written": 2 * n, "ms": mean_ms,
+            "gbs": 4 * n / (mean_ms * 1e-3) / 1e9}
+
+
 def cpu_leg(args, cfg):
     """Oracle (fp32 restatement of reference_simplicial) on evenly spaced query positions."""
     import torch
@@ -208,6 +220,8 @@ def main():
             out["config"] = {"workload": dec["workload"]}
             out["roofline"] = {"bound": "hbm", "achieved": round(dec["achieved_gbs"], 1), "peak": PEAK_HBM_GBS,
                                "unit": "GB/s", "frac": round(dec["hbm_frac"], 4), "traffic": None}
+    if "copy" in legs:
+        out["copy_calibration"] = copy_leg(args)
     if "cpu" in legs:
         cfg = pre["cfg"] if pre is not None and not pre["cfg"].varlen_seqs else W.NS
         out["cpu_baseline"] = cpu_leg(args, cfg)

@@ -137,6 +137,7 @@ int sa_paged_fwd(const sa_paged_args* a, void* workspace, size_t workspace_bytes
   const int splits = sa::paged_choose_splits(a);
   const size_t need = sa::paged_workspace_bytes(a, splits);
   if (workspace_bytes < need) return sa::fail(SA_ERR_INVALID, "workspace too small");
+  if (need && !workspace) return sa::fail(SA_ERR_INVALID, "null workspace");
   if (need && ((uintptr_t)workspace & 255)) return sa::fail(SA_ERR_INVALID, "workspace must be 256-byte aligned");
   hipError_t e = sa::launch_paged(a, splits, workspace, workspace_bytes, (hipStream_t)stream);
   if (e != hipSuccess) return sa::fail(SA_ERR_HIP, hipGetErrorString(e));

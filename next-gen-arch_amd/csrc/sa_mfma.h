@@ -9,12 +9,11 @@
 //   O^T += V^T · P^T        D/32 x 2 MFMAs; the V^T operand is read from the
 //                           natural [key][d] tile with ds_read_b64_tr_b16
 //
-// LDS tiles: K and V, each [rows][D] bf16, row-major, no padding.  The
-// 16-byte segment s of row r is stored at segment s ^ (r & SWZ) so that the
-// 32 lanes reading one segment of 32 consecutive rows hit distinct banks.
+// LDS tiles: K and V, each [rows][D] bf16, row-major with a 32-byte pad per
+// row (see TileGeom).
 //
 // Tiles are filled with global_load_lds_dwordx4 (16 bytes per lane straight
-// into LDS, no staging registers); each DMA instruction covers 512/D rows.
+// into LDS, no staging registers); one instruction fills 1 KB of LDS.
 // The compiler does not order these DMA writes against later LDS reads, so
 // the kernels wait explicitly (vmcnt) before the barrier that publishes a tile.
 #pragma once
@@ -28,25 +27,39 @@ typedef short shortx8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
 
-template <int D>
-struct Tile {
-  static constexpr int kSegs = D / 8;                         // 16-byte segments per row
-  static constexpr int kSwz = (kSegs < 16 ? kSegs : 16) - 1;  // XOR mask of the segment swizzle
-  static constexpr int kRowBytes = 2 * D;
-  static constexpr int kRowsPerDma = 512 / D;                 // rows one 64-lane DMA instruction covers
-  __device__ static __forceinline__ int swz(int row) { return row & kSwz; }
-  __device__ static __forceinline__ int seg_off(int row, int seg) { return row * kRowBytes + ((seg ^ swz(row)) << 4); }
-};
+// LDS tile geometry.  K and V tiles are [rows][D] bf16 with a row stride of
+// 2D + 32 bytes: the 32-byte pad shifts consecutive rows by 8 banks, which
+// keeps both the 16-byte K reads (32 rows, one segment) and the 8-byte
+// transposing V reads (4 rows x 32 bytes per 16 lanes) free of bank
+// conflicts, and every read address is a per-lane base plus an immediate.
+template <int D, int ROWS_T, int NW, int PAD = 32>
+struct TileGeom {
+  static constexpr int kSegs = D / 8;                      // 16-byte segments per row
+  static constexpr int RS = 2 * D + PAD;                   // LDS row stride (bytes)
+  static constexpr int TB = ROWS_T * RS;                   // one tensor tile (bytes)
+  static constexpr int kTensorInstr = (TB + 1023) / 1024;  // DMA instructions per tensor tile
+  static constexpr int kInstr = (2 * kTensorInstr + NW - 1) / NW * NW;
+  static constexpr int NI = kInstr / NW;                   // DMA instructions per wave per tile
+  static constexpr int VOFF = kTensorInstr * 1024;         // V tile offset inside a slot
+  static constexpr int SLOT = kInstr * 1024;               // bytes of one ring slot
 
-// Smallest row count >= need that is a multiple of the DMA row granularity and
-// whose K+V instruction count divides evenly over `waves` waves (uniform vmcnt).
-template <int D>
-__host__ __device__ constexpr int tile_rows(int need, int waves) {
-  int rpi = 512 / D;
-  int r = (need + rpi - 1) / rpi * rpi;
-  while ((2 * r / rpi) % waves) r += rpi;
-  return r;
-}
+  // DMA instruction k of wave `wid` fills LDS bytes [1024*(wid*NI + k), +1024)
+  // of the slot; instructions 0..kTensorInstr-1 fill the K tile, the next
+  // kTensorInstr the V tile, any further ones are idle (they re-fetch row 0
+  // into the unused tail).  Lane `lane` fetches row `row`, segment `seg` of
+  // tensor is_v.  Pad bytes fetch segment 0 of their row (never read).
+  __device__ static __forceinline__ void decode(int wid, int k, int lane, int& is_v, int& row, int& seg) {
+    const int i = wid * NI + k;
+    is_v = i >= kTensorInstr;
+    int b = (is_v ? i - kTensorInstr : i) * 1024 + lane * 16;
+    if (i >= 2 * kTensorInstr || b >= TB) b = 0;
+    row = b / RS;
+    seg = (b % RS) >> 4;
+    if (seg >= kSegs) seg = 0;
+  }
+  __device__ static __forceinline__ bool instr_is_v(int wid, int k) { return wid * NI + k >= kTensorInstr; }
+  __device__ static __forceinline__ char* dst(char* slot, int wid, int k) { return slot + (wid * NI + k) * 1024; }
+};
 
 // s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding:
 // vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
@@ -54,6 +67,21 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Wait until at most k later tiles (NI DMA instructions each) are in flight.
+template <int NI, int P>
+__device__ __forceinline__ void wait_tiles(int k) {
+  if constexpr (P >= 4) {
+    if (k >= 3) { wait_vmcnt<NI * 3>(); return; }
+  }
+  if constexpr (P >= 3) {
+    if (k >= 2) { wait_vmcnt<NI * 2>(); return; }
+  }
+  if constexpr (P >= 2) {
+    if (k >= 1) { wait_vmcnt<NI>(); return; }
+  }
+  wait_vmcnt<0>();
 }
 
 // Barrier without the memory fences of __syncthreads.  Ordering of the DMA
@@ -64,31 +92,8 @@ __device__ __forceinline__ void block_barrier() {
   __builtin_amdgcn_s_barrier();
 }
 
-// Issue the DMA loads of one K/V tile of ROWS rows into `slot` (K tile at
-// slot, V tile at slot + ROWS*2D).  row_off(r, is_v) gives the element offset
-// of tile row r in kbase / vbase (the caller maps rows outside the tensor to a
-// valid row; such rows are masked out of the softmax).  Each of the NW waves
-// issues exactly 2*ROWS/(512/D)/NW instructions.
-template <int D, int ROWS, int NW, typename RowFn>
-__device__ __forceinline__ void issue_tile(char* slot, const bf16* __restrict__ kbase, const bf16* __restrict__ vbase,
-                                           int wid, int lane, RowFn row_off) {
-  using T = Tile<D>;
-  constexpr int per_tensor = ROWS / T::kRowsPerDma;
-  constexpr int total = 2 * per_tensor;
-  static_assert(ROWS % T::kRowsPerDma == 0 && total % NW == 0, "uniform DMA split");
-  const int rsub = lane / T::kSegs;  // row within the instruction
-  const int pseg = lane % T::kSegs;  // LDS segment position this lane fills
-#pragma unroll
-  for (int k = 0; k < total / NW; ++k) {
-    const int i = wid + k * NW;
-    const bool is_v = i >= per_tensor;
-    const int rg = is_v ? i - per_tensor : i;
-    const int row = rg * T::kRowsPerDma + rsub;
-    const int gseg = pseg ^ T::swz(row);
-    const bf16* src = (is_v ? vbase : kbase) + row_off(row, is_v) + gseg * 8;
-    char* dst = slot + (is_v ? ROWS * T::kRowBytes : 0) + rg * T::kRowsPerDma * T::kRowBytes;
-    __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)dst, 16, 0, 0);
-  }
+__device__ __forceinline__ void dma16(const void* src, char* dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void*)dst, 16, 0, 0);
 }
 
 // Per-wave state for 32 A rows.
@@ -110,40 +115,59 @@ struct RowBlock {
   // (used to keep the softmax scale non-negative).  k1 == nullptr -> zero row.
   __device__ __forceinline__ void form_a(const bf16* __restrict__ q, const bf16* __restrict__ k1, int half,
                                          bool q_neg) {
+    if (k1 == nullptr) {
 #pragma unroll
-    for (int t = 0; t < D / 16; ++t) {
-      if (k1 == nullptr) {
-        a[t] = bf16x8{};
-        continue;
-      }
-      const int d0 = 16 * t + 8 * half;
-      bf16x8 qv = *(const bf16x8*)(q + d0);
-      bf16x8 kv = *(const bf16x8*)(k1 + d0);
-      bf16x8 r;
+      for (int t = 0; t < D / 16; ++t) a[t] = bf16x8{};
+      return;
+    }
+    // two fragments in flight at a time (an unconstrained schedule issues all
+    // 2*D/16 loads first, which sets the kernel's register peak)
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        float x = (float)qv[u] * (float)kv[u];
-        r[u] = (bf16)(q_neg ? -x : x);
+    for (int t = 0; t < D / 16; t += 2) {
+      bf16x8 qv[2], kv[2];
+#pragma unroll
+      for (int i = 0; i < 2 && t + i < D / 16; ++i) {
+        const int d0 = 16 * (t + i) + 8 * half;
+        qv[i] = *(const bf16x8*)(q + d0);
+        kv[i] = *(const bf16x8*)(k1 + d0);
       }
-      a[t] = r;
+#pragma unroll
+      for (int i = 0; i < 2 && t + i < D / 16; ++i) {
+        bf16x8 r;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          float x = (float)qv[i][u] * (float)kv[i][u];
+          r[u] = (bf16)(q_neg ? -x : x);
+        }
+        a[t + i] = r;
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
   // One 32-key chunk: tile rows row0 .. row0+31 of the K tile at `ktile` and
-  // the V tile at `vtile`.  sl2 = |scale|*log2(e) >= 0.  key_lo/key_hi: range
-  // of valid chunk keys (0..31) for this wave's query; masking is applied only
-  // when the chunk is not fully valid.
+  // the V tile at `vtile` (row stride RS bytes).  sl2 = |scale|*log2(e) >= 0.
+  // key_lo/key_hi: range of valid chunk keys (0..31) for this wave's query;
+  // masking is applied only when the chunk is not fully valid.
+  template <int RS>
   __device__ __forceinline__ void chunk(const char* ktile, const char* vtile, int row0, int lane, float sl2,
                                         int key_lo, int key_hi) {
-    using T = Tile<D>;
     const int n = lane & 31, half = lane >> 5;
     floatx16 s = floatx16{};
     {
-      const int row = row0 + n;
+      // K fragments are read one step ahead of their MFMA; the scheduling
+      // barriers stop the compiler from hoisting all D/16 reads (which would
+      // hold D/4 extra VGPRs live).
+      const char* kp = ktile + (row0 + n) * RS + 16 * half;
+      bf16x8 kf = *(const bf16x8*)kp;
 #pragma unroll
       for (int t = 0; t < D / 16; ++t) {
-        bf16x8 kf = *(const bf16x8*)(ktile + T::seg_off(row, 2 * t + half));
+        bf16x8 kn;
+        if (t + 1 < D / 16) kn = *(const bf16x8*)(kp + 32 * (t + 1));
+        __builtin_amdgcn_sched_barrier(0);
         s = mfma32x32x16(kf, a[t], s);
+        __builtin_amdgcn_sched_barrier(0);
+        kf = kn;
       }
     }
     const bool masked = key_lo > 0 || key_hi < kChunk - 1;
@@ -200,19 +224,27 @@ struct RowBlock {
     // and keys 16t + 4*half + {0..3} (+8 for the second read).
     const int g16 = (lane >> 4) & 1, i16 = lane & 15;
     const int e_src = i16 >> 2, q_src = i16 & 3;
+    const char* vp = vtile + (row0 + 4 * half + e_src) * RS + 32 * g16 + 8 * q_src;
+    // V fragments, also read one step ahead of their MFMA
+    auto vread = [&](int step) -> bf16x8 {
+      const int t = step / (D / 32), db = step % (D / 32);
+      const char* p1 = vp + 16 * t * RS + 64 * db;
+      shortx4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)p1);
+      shortx4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(p1 + 8 * RS));
+      shortx8 vv = {v1[0], v1[1], v1[2], v1[3], v2[0], v2[1], v2[2], v2[3]};
+      return __builtin_bit_cast(bf16x8, vv);
+    };
+    constexpr int kSteps = 2 * (D / 32);
+    bf16x8 vf = vread(0);
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int r1 = row0 + 16 * t + 4 * half + e_src;
-      const int r2 = r1 + 8;
-#pragma unroll
-      for (int db = 0; db < D / 32; ++db) {
-        const int seg = 4 * db + 2 * g16 + (q_src >> 1);
-        const int sub = (q_src & 1) * 8;
-        shortx4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(vtile + T::seg_off(r1, seg) + sub));
-        shortx4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(vtile + T::seg_off(r2, seg) + sub));
-        shortx8 vv = {v1[0], v1[1], v1[2], v1[3], v2[0], v2[1], v2[2], v2[3]};
-        o[db] = mfma32x32x16(__builtin_bit_cast(bf16x8, vv), pb[t], o[db]);
-      }
+    for (int step = 0; step < kSteps; ++step) {
+      bf16x8 vn;
+      if (step + 1 < kSteps) vn = vread(step + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      const int t = step / (D / 32), db = step % (D / 32);
+      o[db] = mfma32x32x16(vf, pb[t], o[db]);
+      __builtin_amdgcn_sched_barrier(0);
+      vf = vn;
     }
   }
 };

@@ -49,17 +49,20 @@ struct PagedParams {
   float* part_o;  // [P][tokens][hq][D], P = splits * nr
   float* part_m;  // [P][tokens][hq]
   float* part_z;
+  int direct;     // splits * nr == 1: write out / lse directly, no partials
+  float* out;
+  int64_t o_st, o_sh;
+  float* lse;
 };
 
 constexpr int kPageCache = 256;  // page ids of one split kept in LDS
 
 template <int D, int NW, int P>
 __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel(PagedParams p) {
-  using T = Tile<D>;
-  constexpr int ROWS = kChunk;
-  constexpr int SLOT = 2 * ROWS * T::kRowBytes;
+  using G = TileGeom<D, kChunk, NW>;
+  constexpr int SLOT = G::SLOT;
   constexpr int R = P + 1;
-  constexpr int NI = 2 * ROWS / T::kRowsPerDma / NW;  // DMA instructions per wave per tile
+  constexpr int NI = G::NI;  // DMA instructions per wave per tile
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -99,11 +102,8 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
   };
 
   RowBlock<D> rb;
-  rb.reset();
   const int j = pos - 32 * r - n;
   const bool row_ok = task_ok && j >= lo1 && cbeg < cend;
-  const bf16* k1row = row_ok ? p.sc + row_off(p.stable, p.st_s, p.st_w, p.s_blocks, p.sc_b, p.sc_s, p.sc_h, j) : nullptr;
-  rb.form_a(p.q + (int64_t)token * p.q_st + (int64_t)h * p.q_sh, k1row, half, p.q_neg != 0);
 
   // The page ids of this split's long-window rows are staged in LDS first:
   // a block-table load inside the pipeline would be a vector load whose
@@ -124,37 +124,47 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
   // tile rows outside [lo2, pos] re-read the nearest valid row (masked later)
   auto issue = [&](int c) {
     const int k0 = kstart + kChunk * c;
-    issue_tile<D, ROWS, NW>(lds + (c % R) * SLOT, p.lc, p.lc + p.lc_a, wid, lane, [&](int row, bool) -> int64_t {
+    char* slot = lds + (c % R) * SLOT;
+#pragma unroll
+    for (int k = 0; k < NI; ++k) {
+      int is_v, row, seg;
+      G::decode(wid, k, lane, is_v, row, seg);
       const int ps = min(max(k0 + row, lo2), pos);
       const int pg = ps / p.bs;
       const int64_t blk = cached ? pcache[pg - page_lo]
                                  : block_of(p.ltable, p.table64, p.lt_s, p.lt_w, p.l_blocks, seq, ps, p.bs);
-      return blk * p.lc_b + (int64_t)(ps - pg * p.bs) * p.lc_s + (int64_t)g * p.lc_h;
-    });
+      const int64_t off = blk * p.lc_b + (int64_t)(ps - pg * p.bs) * p.lc_s + (int64_t)g * p.lc_h +
+                          (is_v ? p.lc_a : 0) + seg * 8;
+      dma16(p.lc + off, G::dst(slot, wid, k));
+    }
   };
 
   if (cbeg < cend) {
 #pragma unroll
     for (int e = 0; e < P; ++e)
       if (cbeg + e < cend) issue(cbeg + e);
+    // A rows after the tile loads are in flight: the k1 gathers overlap them
+    const bf16* k1row =
+        row_ok ? p.sc + row_off(p.stable, p.st_s, p.st_w, p.s_blocks, p.sc_b, p.sc_s, p.sc_h, j) : nullptr;
+    rb.form_a(p.q + (int64_t)token * p.q_st + (int64_t)h * p.q_sh, k1row, half, p.q_neg != 0);
+    rb.reset();
     for (int c = cbeg; c < cend; ++c) {
-      const int ahead = min(P - 1, cend - 1 - c);
-      if constexpr (P >= 4) { if (ahead >= 3) wait_vmcnt<3 * NI>(); else if (ahead == 2) wait_vmcnt<2 * NI>(); else if (ahead == 1) wait_vmcnt<NI>(); else wait_vmcnt<0>(); }
-      else if constexpr (P == 3) { if (ahead >= 2) wait_vmcnt<2 * NI>(); else if (ahead == 1) wait_vmcnt<NI>(); else wait_vmcnt<0>(); }
-      else if constexpr (P == 2) { if (ahead >= 1) wait_vmcnt<NI>(); else wait_vmcnt<0>(); }
-      else { wait_vmcnt<0>(); }
+      wait_tiles<NI, P>(min(P - 1, cend - 1 - c));
       block_barrier();
       if (c + P < cend) issue(c + P);
-      if (task_ok) {
-        const int kfirst = kstart + kChunk * c;
-        const char* slot = lds + (c % R) * SLOT;
-        rb.chunk(slot, slot + ROWS * T::kRowBytes, 0, lane, p.sl2, max(lo2 - kfirst, 0), min(pos - kfirst, kChunk - 1));
-      }
+      // unconditional (see the prefill kernel): idle waves get an empty key range
+      const int kfirst = kstart + kChunk * c;
+      const char* slot = lds + (c % R) * SLOT;
+      rb.template chunk<G::RS>(slot, slot + G::VOFF, 0, lane, p.sl2, task_ok ? max(lo2 - kfirst, 0) : kChunk,
+                               task_ok ? min(pos - kfirst, kChunk - 1) : -1);
     }
     block_barrier();
+  } else {
+    rb.reset();
   }
 
-  // ---- epilogue: merge this wave's 32 rows, write one partial
+  // ---- epilogue: merge this wave's 32 rows, write one partial (or, when
+  // this workgroup is the only contributor, the final output)
   const float zrow = pair_sum(rb.z);
   const float mrow = row_ok ? rb.m : -INFINITY;
   const float Mw = wave_max(mrow);
@@ -186,11 +196,18 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
       acc += (x[0] + x[1]) + (x[2] + x[3]);
     }
     block_barrier();
-    if (task_ok) p.part_o[prow * D + 64 * sl + lane] = acc;
+    if (task_ok) {
+      if (p.direct) p.out[(int64_t)token * p.o_st + (int64_t)h * p.o_sh + 64 * sl + lane] = acc / Zw;
+      else p.part_o[prow * D + 64 * sl + lane] = acc;
+    }
   }
   if (task_ok && lane == 0) {
-    p.part_m[prow] = Mw;
-    p.part_z[prow] = Zw;
+    if (p.direct) {
+      if (p.lse) p.lse[(int64_t)token * p.hq + h] = (Mw + __log2f(Zw)) * kLn2;
+    } else {
+      p.part_m[prow] = Mw;
+      p.part_z[prow] = Zw;
+    }
   }
 }
 
@@ -287,17 +304,19 @@ int paged_choose_splits(const sa_paged_args* a) {
   const int tasks = group * ((a->short_window + 31) / 32);
   const int nw = paged_nw(a);
   const int64_t wgs = (int64_t)a->tokens * a->heads_kv * ((tasks + nw - 1) / nw);
-  const int64_t target = 8LL * device_cu_count();
+  // Two resident workgroups per CU keep enough tile loads in flight; split
+  // the long window only when (token, KV group) pairs alone cannot fill that.
+  const int64_t target = 2LL * device_cu_count();
   int s = (int)((target + wgs - 1) / wgs);
   if (s < 1) s = 1;
-  // at least 2 chunks per split keeps the double buffer useful
-  int cap = nc / 2 > 0 ? nc / 2 : 1;
+  int cap = nc / 2 > 0 ? nc / 2 : 1;  // at least 2 chunks per split
   if (s > cap) s = cap;
   return s;
 }
 
 size_t paged_workspace_bytes(const sa_paged_args* a, int splits) {
   if (!paged_mfma_supported(a)) return 0;
+  if (splits * ((a->short_window + 31) / 32) == 1) return 0;  // direct output, no partials
   const size_t P = (size_t)splits * ((a->short_window + 31) / 32);
   const size_t th = (size_t)a->tokens * a->heads_q;
   size_t b = P * th * (size_t)a->head_dim * 4;
@@ -306,12 +325,12 @@ size_t paged_workspace_bytes(const sa_paged_args* a, int splits) {
   return b + 2 * m;
 }
 
-constexpr int kPagedDepth = 3;  // tiles in flight per workgroup
+constexpr int kPagedDepth = 2;  // tiles in flight per workgroup (2 workgroups fit one CU)
 
 template <int D, int NW>
 static hipError_t launch_paged_mfma_t(PagedParams p, hipStream_t stream) {
   constexpr int P = D >= 256 ? 2 : kPagedDepth;
-  const size_t lds_ring = (size_t)(P + 1) * 2 * kChunk * Tile<D>::kRowBytes + kPageCache * sizeof(int64_t);
+  const size_t lds_ring = (size_t)(P + 1) * TileGeom<D, kChunk, NW>::SLOT + kPageCache * sizeof(int64_t);
   const size_t lds_red = (size_t)NW * 64 * 36 * sizeof(float);
   const size_t lds = lds_ring > lds_red ? lds_ring : lds_red;
   auto kern = paged_mfma_kernel<D, NW, P>;
@@ -376,13 +395,20 @@ hipError_t launch_paged(const sa_paged_args* a, int splits, void* ws, size_t ws_
     p.tblocks = (p.tasks + nw - 1) / nw;
     const size_t P = (size_t)splits * p.nr;
     const size_t th = (size_t)a->tokens * a->heads_q;
-    char* w = (char*)ws;
-    size_t ob = (P * th * (size_t)a->head_dim * 4 + 255) & ~(size_t)255;
-    size_t mb = (P * th * 4 + 255) & ~(size_t)255;
-    if (ws_bytes < ob + 2 * mb || ((uintptr_t)ws & 255)) return hipErrorInvalidValue;
-    p.part_o = (float*)w;
-    p.part_m = (float*)(w + ob);
-    p.part_z = (float*)(w + ob + mb);
+    p.direct = P == 1;
+    p.out = a->out;
+    p.o_st = a->o_stride_t;
+    p.o_sh = a->o_stride_h;
+    p.lse = a->lse;
+    if (!p.direct) {
+      char* w = (char*)ws;
+      size_t ob = (P * th * (size_t)a->head_dim * 4 + 255) & ~(size_t)255;
+      size_t mb = (P * th * 4 + 255) & ~(size_t)255;
+      if (ws_bytes < ob + 2 * mb || ((uintptr_t)ws & 255)) return hipErrorInvalidValue;
+      p.part_o = (float*)w;
+      p.part_m = (float*)(w + ob);
+      p.part_z = (float*)(w + ob + mb);
+    }
     hipError_t e;
     switch (a->head_dim) {
       case 64: e = launch_paged_mfma_d<64>(p, nw, stream); break;
@@ -390,6 +416,7 @@ hipError_t launch_paged(const sa_paged_args* a, int splits, void* ws, size_t ws_
       default: e = launch_paged_mfma_d<256>(p, nw, stream); break;
     }
     if (e != hipSuccess) return e;
+    if (p.direct) return hipSuccess;
     const int64_t nth = (int64_t)a->tokens * a->heads_q;
     hipLaunchKernelGGL(paged_combine_kernel, dim3((unsigned)((nth + 3) / 4)), dim3(256), 0, stream, p.part_o,
                        p.part_m, p.part_z, (int)P, a->tokens, a->heads_q, a->head_dim, a->out, a->o_stride_t,

@@ -73,31 +73,22 @@ __device__ __forceinline__ int xcd_remap(int b, int n) {
   return x * q + min(x, r) + i;
 }
 
-// Wait until at most k later tiles (NI DMA instructions each) are in flight.
-template <int NI, int P>
-__device__ __forceinline__ void wait_tiles(int k) {
-  if constexpr (P >= 4) {
-    if (k >= 3) { wait_vmcnt<NI * 3>(); return; }
-  }
-  if constexpr (P >= 3) {
-    if (k >= 2) { wait_vmcnt<NI * 2>(); return; }
-  }
-  if constexpr (P >= 2) {
-    if (k >= 1) { wait_vmcnt<NI>(); return; }
-  }
-  wait_vmcnt<0>();
-}
+#ifndef SA_PREFILL_WAVES_PER_SIMD
+#define SA_PREFILL_WAVES_PER_SIMD 2
+#endif
+#ifndef SA_PREFILL_DEPTH
+#define SA_PREFILL_DEPTH 3
+#endif
 
 template <int D, int NQ, int NH, int P>
-__global__ __launch_bounds__(256, (D >= 256 ? 1 : 2)) void prefill_mfma_kernel(PrefillParams p) {
+__global__ __launch_bounds__(256, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_SIMD)) void prefill_mfma_kernel(PrefillParams p) {
   static_assert(NQ * NH == 4, "4 waves per block");
   static_assert(P >= 1 && P <= 4, "prefetch depth");
-  using T = Tile<D>;
   constexpr int NW = 4;
-  constexpr int ROWS = tile_rows<D>(kChunk + NQ - 1, NW);
-  constexpr int SLOT = 2 * ROWS * T::kRowBytes;
+  constexpr int ROWS = kChunk + NQ - 1;  // tile rows: one chunk of all NQ queries
+  using G = TileGeom<D, ROWS, NW>;
   constexpr int R = P + 1;
-  constexpr int NI = 2 * ROWS / T::kRowsPerDma / NW;  // DMA instructions per wave per tile
+  constexpr int NI = G::NI;
   extern __shared__ __attribute__((aligned(16))) char lds[];
 
   const int tid = threadIdx.x;
@@ -137,12 +128,34 @@ __global__ __launch_bounds__(256, (D >= 256 ? 1 : 2)) void prefill_mfma_kernel(P
   const int last = p.total - 1;
   const int64_t k_st = p.k_st, v_st = p.v_st;
   const int64_t k_g = (int64_t)g * p.k_sh, v_g = (int64_t)g * p.v_sh;
+
+  // Per lane and DMA instruction: byte offset of its 16 bytes from the tile's
+  // first row (interior tiles: uniform base + this offset).
+  uint32_t voff[NI];
+#pragma unroll
+  for (int k = 0; k < NI; ++k) {
+    int is_v, row, seg;
+    G::decode(wid, k, lane, is_v, row, seg);
+    voff[k] = (uint32_t)(((int64_t)row * (is_v ? v_st : k_st) + seg * 8) * 2);
+  }
   auto issue = [&](int c) {
-    const int key0 = kb0 + kChunk * c;
-    issue_tile<D, ROWS, NW>(lds + (c % R) * SLOT, p.k2, p.v2, wid, lane, [&](int row, bool is_v) -> int64_t {
-      const int key = min(max(key0 + row, 0), last);
-      return is_v ? (int64_t)key * v_st + v_g : (int64_t)key * k_st + k_g;
-    });
+    char* slot = lds + (c % R) * G::SLOT;
+    const int kb = __builtin_amdgcn_readfirstlane(kb0 + kChunk * c);  // uniform: scalar test and tile bases
+    if (kb >= 0 && kb + ROWS - 1 <= last) {
+      const char* kbase = (const char*)(p.k2 + (int64_t)kb * k_st + k_g);
+      const char* vbase = (const char*)(p.v2 + (int64_t)kb * v_st + v_g);
+#pragma unroll
+      for (int k = 0; k < NI; ++k) dma16((G::instr_is_v(wid, k) ? vbase : kbase) + voff[k], G::dst(slot, wid, k));
+    } else {  // tile crosses the tensor edge: clamp every row into [0, total)
+#pragma unroll
+      for (int k = 0; k < NI; ++k) {
+        int is_v, row, seg;
+        G::decode(wid, k, lane, is_v, row, seg);
+        const int64_t key = min(max(kb + row, 0), last);
+        const bf16* src = is_v ? p.v2 + key * v_st + v_g : p.k2 + key * k_st + k_g;
+        dma16(src + seg * 8, G::dst(slot, wid, k));
+      }
+    }
   };
 
   const int half = lane >> 5, n = lane & 31;
@@ -157,9 +170,9 @@ __global__ __launch_bounds__(256, (D >= 256 ? 1 : 2)) void prefill_mfma_kernel(P
   for (int r = 0; r < p.nr; ++r) {
     const int j = t - 32 * r - n;  // this lane's short-axis key
     const bool row_ok = qvalid && j >= lo1;
-    rb.reset();
     rb.form_a(p.q + (int64_t)t * p.q_st + (int64_t)h * p.q_sh,
               row_ok ? p.k1 + (int64_t)j * k_st + k_g : nullptr, half, p.q_neg != 0);
+    rb.reset();
 
 #pragma unroll
     for (int e = 0; e < P; ++e)
@@ -168,12 +181,15 @@ __global__ __launch_bounds__(256, (D >= 256 ? 1 : 2)) void prefill_mfma_kernel(P
       wait_tiles<NI, P>(min(P - 1, p.nc - 1 - c));
       block_barrier();  // tile c complete for every wave; slot of tile c-1 free
       if (c + P < p.nc) issue(c + P);
-      if (qvalid && c >= cfirst) {
-        const int kfirst = t - p.wl + 1 + kChunk * c;  // key of this wave's chunk row 0
-        const char* slot = lds + (c % R) * SLOT;
-        rb.chunk(slot, slot + ROWS * T::kRowBytes, qo, lane, p.sl2, max(lo2 - kfirst, 0),
-                 min(t - kfirst, kChunk - 1));
-      }
+      // Unconditional: a wave without valid keys in this step gets an empty
+      // key range (every p = 0, an exact no-op).  A branch here would give
+      // the accumulators two incoming values at the loop latch, which the
+      // register allocator resolves by keeping a second copy of all of O.
+      const bool active = qvalid && c >= cfirst;
+      const int kfirst = t - p.wl + 1 + kChunk * c;  // key of this wave's chunk row 0
+      const char* slot = lds + (c % R) * G::SLOT;
+      rb.template chunk<G::RS>(slot, slot + G::VOFF, qo, lane, p.sl2, active ? max(lo2 - kfirst, 0) : kChunk,
+                               active ? min(t - kfirst, kChunk - 1) : -1);
     }
     block_barrier();  // ring reads done: LDS reused below
 
@@ -249,8 +265,8 @@ static hipError_t launch_prefill_mfma(const PrefillParams& base_p, hipStream_t s
   p.qblocks = (p.total + NQ - 1) / NQ;
   p.hsub = p.group / NH;
   p.nblocks = p.qblocks * p.hk * p.hsub;
-  constexpr int ROWS = tile_rows<D>(kChunk + NQ - 1, 4);
-  size_t lds = (size_t)(P + 1) * 2 * ROWS * Tile<D>::kRowBytes;
+  using G = TileGeom<D, kChunk + NQ - 1, 4>;
+  size_t lds = (size_t)(P + 1) * G::SLOT;
   const size_t red = (size_t)4 * 64 * 36 * sizeof(float);
   if (lds < red) lds = red;
   auto kern = prefill_mfma_kernel<D, NQ, NH, P>;
@@ -270,9 +286,10 @@ static hipError_t dispatch_prefill_mfma_d(const PrefillParams& p, hipStream_t st
     if (G % 2 == 0) return launch_prefill_mfma<D, 2, 2, 2>(p, stream);
     return launch_prefill_mfma<D, 4, 1, 2>(p, stream);
   } else {
-    if (G % 4 == 0) return launch_prefill_mfma<D, 1, 4, 4>(p, stream);
-    if (G % 2 == 0) return launch_prefill_mfma<D, 2, 2, 3>(p, stream);
-    return launch_prefill_mfma<D, 4, 1, 3>(p, stream);
+    constexpr int P = SA_PREFILL_DEPTH;
+    if (G % 4 == 0) return launch_prefill_mfma<D, 1, 4, P>(p, stream);
+    if (G % 2 == 0) return launch_prefill_mfma<D, 2, 2, P>(p, stream);
+    return launch_prefill_mfma<D, 4, 1, P>(p, stream);
   }
 }
 
