@@ -18,6 +18,8 @@
 // the kernels wait explicitly (vmcnt) before the barrier that publishes a tile.
 #pragma once
 
+#include <type_traits>
+
 #include "sa_common.h"
 
 namespace sa {
@@ -96,6 +98,38 @@ __device__ __forceinline__ void dma16(const void* src, char* dst) {
   __builtin_amdgcn_global_load_lds(src, (lds_void*)dst, 16, 0, 0);
 }
 
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// 32-bit LDS address of a pointer into the workgroup's LDS.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// ds_read_b64_tr_b16 issued through inline asm.  The compiler builtin makes
+// the backend wait for every outstanding global->LDS DMA (vmcnt(0)) before
+// each transposing read, which would drain the tile prefetch queue; the DMA
+// ordering is already enforced explicitly (vmcnt wait + barrier per tile).
+// The result is only valid after lds_wait() on it.
+template <int OFF>
+__device__ __forceinline__ shortx4 ds_read_tr16(uint32_t addr) {
+  shortx4 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+
+// Wait for this wave's LDS reads; the operands tie the wait to the registers
+// those reads fill, so no use of them can be scheduled before it.
+__device__ __forceinline__ void lds_wait(shortx4& a, shortx4& b) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b));
+}
+
 // Per-wave state for 32 A rows.
 template <int D>
 struct RowBlock {
@@ -120,29 +154,31 @@ struct RowBlock {
       for (int t = 0; t < D / 16; ++t) a[t] = bf16x8{};
       return;
     }
-    // two fragments in flight at a time (an unconstrained schedule issues all
-    // 2*D/16 loads first, which sets the kernel's register peak)
+    // all 2*D/16 fragment loads are issued before the first use (one memory
+    // round trip); this runs before the accumulators are initialised
 #pragma unroll
-    for (int t = 0; t < D / 16; t += 2) {
-      bf16x8 qv[2], kv[2];
+    for (int t = 0; t < D / 16; ++t) {
+      const int d0 = 16 * t + 8 * half;
+      const bf16x8 qv = *(const bf16x8*)(q + d0);
+      const bf16x8 kv = *(const bf16x8*)(k1 + d0);
+      bf16x8 r;
 #pragma unroll
-      for (int i = 0; i < 2 && t + i < D / 16; ++i) {
-        const int d0 = 16 * (t + i) + 8 * half;
-        qv[i] = *(const bf16x8*)(q + d0);
-        kv[i] = *(const bf16x8*)(k1 + d0);
+      for (int u = 0; u < 8; ++u) {
+        const float x = (float)qv[u] * (float)kv[u];
+        r[u] = (bf16)(q_neg ? -x : x);
       }
-#pragma unroll
-      for (int i = 0; i < 2 && t + i < D / 16; ++i) {
-        bf16x8 r;
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          float x = (float)qv[i][u] * (float)kv[i][u];
-          r[u] = (bf16)(q_neg ? -x : x);
-        }
-        a[t + i] = r;
-      }
-      __builtin_amdgcn_sched_barrier(0);
+      a[t] = r;
     }
+  }
+
+  // The two transposing reads of V fragment `step` (t = step / (D/32) selects
+  // keys 16t.., db = step % (D/32) the 32-wide d block).
+  template <int RS, int STEP>
+  __device__ static __forceinline__ void vread(uint32_t vp, shortx4& v1, shortx4& v2) {
+    constexpr int t = STEP / (D / 32), db = STEP % (D / 32);
+    constexpr int off = 16 * t * RS + 64 * db;
+    v1 = ds_read_tr16<off>(vp);
+    v2 = ds_read_tr16<off + 8 * RS>(vp);
   }
 
   // One 32-key chunk: tile rows row0 .. row0+31 of the K tile at `ktile` and
@@ -224,28 +260,27 @@ struct RowBlock {
     // and keys 16t + 4*half + {0..3} (+8 for the second read).
     const int g16 = (lane >> 4) & 1, i16 = lane & 15;
     const int e_src = i16 >> 2, q_src = i16 & 3;
-    const char* vp = vtile + (row0 + 4 * half + e_src) * RS + 32 * g16 + 8 * q_src;
-    // V fragments, also read one step ahead of their MFMA
-    auto vread = [&](int step) -> bf16x8 {
-      const int t = step / (D / 32), db = step % (D / 32);
-      const char* p1 = vp + 16 * t * RS + 64 * db;
-      shortx4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)p1);
-      shortx4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(p1 + 8 * RS));
-      shortx8 vv = {v1[0], v1[1], v1[2], v1[3], v2[0], v2[1], v2[2], v2[3]};
-      return __builtin_bit_cast(bf16x8, vv);
-    };
+    const uint32_t vp = lds_addr(vtile + (row0 + 4 * half + e_src) * RS + 32 * g16 + 8 * q_src);
+    // V fragments are read one step ahead of their MFMA
     constexpr int kSteps = 2 * (D / 32);
-    bf16x8 vf = vread(0);
-#pragma unroll
-    for (int step = 0; step < kSteps; ++step) {
-      bf16x8 vn;
-      if (step + 1 < kSteps) vn = vread(step + 1);
+    shortx4 v1, v2;
+    vread<RS, 0>(vp, v1, v2);
+    lds_wait(v1, v2);
+    static_for<0, kSteps>([&](auto st) {
+      constexpr int step = decltype(st)::value;
+      shortx8 vv = {v1[0], v1[1], v1[2], v1[3], v2[0], v2[1], v2[2], v2[3]};
+      const bf16x8 vf = __builtin_bit_cast(bf16x8, vv);
+      shortx4 n1, n2;
+      if constexpr (step + 1 < kSteps) vread<RS, step + 1>(vp, n1, n2);
       __builtin_amdgcn_sched_barrier(0);
-      const int t = step / (D / 32), db = step % (D / 32);
-      o[db] = mfma32x32x16(vf, pb[t], o[db]);
+      o[step % (D / 32)] = mfma32x32x16(vf, pb[step / (D / 32)], o[step % (D / 32)]);
       __builtin_amdgcn_sched_barrier(0);
-      vf = vn;
-    }
+      if constexpr (step + 1 < kSteps) {
+        lds_wait(n1, n2);
+        v1 = n1;
+        v2 = n2;
+      }
+    });
   }
 };
 

@@ -55,7 +55,7 @@ struct PagedParams {
   float* lse;
 };
 
-constexpr int kPageCache = 256;  // page ids of one split kept in LDS
+constexpr int kPosCache = 1024;  // long-window positions of one split whose row offsets are kept in LDS
 
 template <int D, int NW, int P>
 __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel(PagedParams p) {
@@ -105,21 +105,29 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
   const int j = pos - 32 * r - n;
   const bool row_ok = task_ok && j >= lo1 && cbeg < cend;
 
-  // The page ids of this split's long-window rows are staged in LDS first:
-  // a block-table load inside the pipeline would be a vector load whose
-  // result feeds a DMA address, and waiting for it would also wait for every
-  // older tile load (vector loads complete in order).
-  int64_t* pcache = (int64_t*)(lds + R * SLOT);
+  // Row offsets (element offset of the K row of head g) of every long-window
+  // position of this split are computed once and kept in LDS: a block-table
+  // load inside the pipeline would be a vector load whose result feeds a DMA
+  // address, and waiting for it would also wait for every older tile load
+  // (vector loads complete in order).  The split count guarantees the
+  // split's positions fit (kPosCache).
+  int64_t* roff = (int64_t*)(lds + R * SLOT);
   const int ps_lo = max(lo2, kstart + kChunk * cbeg);
   const int ps_hi = min(pos, kstart + kChunk * cend - 1);
-  const int page_lo = ps_lo / p.bs;
-  const int npages = ps_hi / p.bs - page_lo + 1;
-  const bool cached = cbeg < cend && npages <= kPageCache;
-  if (cached) {
-    for (int i = tid; i < npages; i += 64 * NW)
-      pcache[i] = block_of(p.ltable, p.table64, p.lt_s, p.lt_w, p.l_blocks, seq, (page_lo + i) * p.bs, p.bs);
+  if (cbeg < cend) {
+    const int npos = min(ps_hi - ps_lo + 1, kPosCache);
+    for (int i = tid; i < npos; i += 64 * NW) {
+      const int ps = ps_lo + i;
+      const int64_t blk = block_of(p.ltable, p.table64, p.lt_s, p.lt_w, p.l_blocks, seq, ps, p.bs);
+      roff[i] = blk * p.lc_b + (int64_t)(ps % p.bs) * p.lc_s + (int64_t)g * p.lc_h;
+    }
     __syncthreads();
   }
+
+  // this lane's tile row / segment / tensor for each of its DMA instructions
+  int drow[NI], dseg[NI], dv[NI];
+#pragma unroll
+  for (int k = 0; k < NI; ++k) G::decode(wid, k, lane, dv[k], drow[k], dseg[k]);
 
   // tile rows outside [lo2, pos] re-read the nearest valid row (masked later)
   auto issue = [&](int c) {
@@ -127,14 +135,8 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
     char* slot = lds + (c % R) * SLOT;
 #pragma unroll
     for (int k = 0; k < NI; ++k) {
-      int is_v, row, seg;
-      G::decode(wid, k, lane, is_v, row, seg);
-      const int ps = min(max(k0 + row, lo2), pos);
-      const int pg = ps / p.bs;
-      const int64_t blk = cached ? pcache[pg - page_lo]
-                                 : block_of(p.ltable, p.table64, p.lt_s, p.lt_w, p.l_blocks, seq, ps, p.bs);
-      const int64_t off = blk * p.lc_b + (int64_t)(ps - pg * p.bs) * p.lc_s + (int64_t)g * p.lc_h +
-                          (is_v ? p.lc_a : 0) + seg * 8;
+      const int ps = min(max(k0 + drow[k], lo2), pos);
+      const int64_t off = roff[min(ps - ps_lo, kPosCache - 1)] + (dv[k] ? p.lc_a : 0) + dseg[k] * 8;
       dma16(p.lc + off, G::dst(slot, wid, k));
     }
   };
@@ -299,7 +301,12 @@ static int paged_nw(const sa_paged_args* a) {
 int paged_choose_splits(const sa_paged_args* a) {
   if (!paged_mfma_supported(a)) return 1;
   const int nc = (int)(((int64_t)a->long_window + kChunk - 1) / kChunk);
-  if (a->splits > 0) return a->splits < nc ? a->splits : nc;
+  // every split's positions must fit the in-kernel row-offset cache
+  const int min_splits = (nc + kPosCache / kChunk - 1) / (kPosCache / kChunk);
+  if (a->splits > 0) {
+    const int s = a->splits < nc ? a->splits : nc;
+    return s > min_splits ? s : min_splits;
+  }
   const int group = a->heads_q / a->heads_kv;
   const int tasks = group * ((a->short_window + 31) / 32);
   const int nw = paged_nw(a);
@@ -311,7 +318,7 @@ int paged_choose_splits(const sa_paged_args* a) {
   if (s < 1) s = 1;
   int cap = nc / 2 > 0 ? nc / 2 : 1;  // at least 2 chunks per split
   if (s > cap) s = cap;
-  return s;
+  return s > min_splits ? s : min_splits;
 }
 
 size_t paged_workspace_bytes(const sa_paged_args* a, int splits) {
@@ -325,12 +332,15 @@ size_t paged_workspace_bytes(const sa_paged_args* a, int splits) {
   return b + 2 * m;
 }
 
-constexpr int kPagedDepth = 2;  // tiles in flight per workgroup (2 workgroups fit one CU)
+#ifndef SA_PAGED_DEPTH
+#define SA_PAGED_DEPTH 1
+#endif
+constexpr int kPagedDepth = SA_PAGED_DEPTH;  // tiles in flight per workgroup (2 workgroups fit one CU)
 
 template <int D, int NW>
 static hipError_t launch_paged_mfma_t(PagedParams p, hipStream_t stream) {
   constexpr int P = D >= 256 ? 2 : kPagedDepth;
-  const size_t lds_ring = (size_t)(P + 1) * TileGeom<D, kChunk, NW>::SLOT + kPageCache * sizeof(int64_t);
+  const size_t lds_ring = (size_t)(P + 1) * TileGeom<D, kChunk, NW>::SLOT + kPosCache * sizeof(int64_t);
   const size_t lds_red = (size_t)NW * 64 * 36 * sizeof(float);
   const size_t lds = lds_ring > lds_red ? lds_ring : lds_red;
   auto kern = paged_mfma_kernel<D, NW, P>;
