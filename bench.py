@@ -32,13 +32,33 @@ PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 def _args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--decode-steps", type=int, default=200)
     ap.add_argument("--legs", default="prefill,decode,cpu")
     ap.add_argument("--workload", default="NS", help="prefill workload: NS, C2, C3, C4")
     ap.add_argument("--cpu-positions", type=int, default=256)
+    ap.add_argument("--cpu-decode-tokens", type=int, default=16)
     return ap.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
+
+
+def measured_traffic(kernel, workload):
+    """HBM bytes per dispatch of `kernel` on `workload` from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE table (KiB per dispatch, each scaled by
+    the factor its counter reads for a copy of known size), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 6 and not line.startswith("#") and parts[0] == kernel and parts[1] == workload:
+                    fetch, write, ff, wf = (float(x) for x in parts[2:])
+                    return 1024.0 * (fetch * ff + write * wf)
+    except OSError:
+        pass
+    return None
 
 
 def _time_kernel(fn, steps, warmup, flush=None):
@@ -107,8 +127,10 @@ def decode_leg(args):
     a = (inp["q"], inp["short_cache"], inp["long_cache"], inp["block_table"], inp["token_seq"], inp["token_pos"])
     kw = dict(short_window=cfg.w2, long_window=cfg.w1, scale=1.0)
     name, splits, ws_bytes = paged_plan(*a, **kw)
-    # reuse one workspace-free call path: the shim allocates from torch's caching allocator
-    flush_buf = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device=dev)
+    # 1 GiB fill between steps: evicts the windows from L2 and the 256 MB MALL,
+    # and runs long enough that the host has queued the next call before the
+    # GPU reaches it (the events then bracket the kernel alone)
+    flush_buf = torch.empty(1024 * 1024 * 1024, dtype=torch.uint8, device=dev)
 
     def flush():
         flush_buf.fill_(1)
@@ -117,17 +139,60 @@ def decode_leg(args):
         return simplicial_paged_attention(*a, return_lse=True, **kw)
     mean_ms, med_ms, _ = _time_kernel(fn, args.decode_steps, max(args.warmup, 10), flush=flush)
     nbytes = W.paged_bytes(cfg, inp["ctx"], out_bytes=4)
-    gbs = nbytes / (mean_ms * 1e-3) / 1e9
+    gbs = nbytes / (med_ms * 1e-3) / 1e9
     res = {
-        "workload": cfg.name, "tokens_per_step": cfg.batch, "us_per_step": mean_ms * 1e3,
-        "median_us_per_step": med_ms * 1e3, "tok_per_s": cfg.batch / (mean_ms * 1e-3),
+        "workload": cfg.name, "tokens_per_step": cfg.batch, "us_per_step": med_ms * 1e3,
+        "mean_us_per_step": mean_ms * 1e3, "tok_per_s": cfg.batch / (med_ms * 1e-3),
         "algorithmic_bytes_per_step": nbytes, "achieved_gbs": gbs, "hbm_frac": gbs / PEAK_HBM_GBS,
         "kernel": name, "splits": splits, "flops_per_step": W.paged_flops(cfg, inp["ctx"]),
         "l2_flushed": True,
     }
+    traffic = measured_traffic("paged_mfma_kernel", "C5")
+    res["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                       "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic}
+    if "cpu" in set(args.legs.split(",")):
+        res["cpu_baseline"] = decode_cpu_leg(args, cfg, inp)
     del inp, flush_buf
     torch.cuda.empty_cache()
     return res
+
+
+def decode_cpu_leg(args, cfg, inp):
+    """Oracle (fp32 restatement of the dense math) on the first tokens of C5:
+    their windows are gathered through the block table on the GPU, copied to
+    the host, and only the CPU evaluation is timed."""
+    import torch
+    from oracle import simplicial_oracle as O
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    n = max(1, min(args.cpu_decode_tokens, cfg.batch))
+    table = inp["block_table"].to(torch.int64)
+
+    def gather(cache, s, lo, hi):
+        pos = torch.arange(lo, hi + 1, device=cache.device)
+        blocks = table[s][pos // cfg.page]
+        return cache[0, blocks, pos % cfg.page], cache[1, blocks, pos % cfg.page]
+
+    work = []
+    for t in range(n):
+        s, p = int(inp["token_seq"][t]), int(inp["token_pos"][t])
+        k1, v1 = gather(inp["short_cache"], s, max(0, p - cfg.w2 + 1), p)
+        k2, v2 = gather(inp["long_cache"], s, max(0, p - cfg.w1 + 1), p)
+        work.append([x.float().cpu() for x in (inp["q"][t], k1, k2, v1, v2)])
+    O._single_query(*work[0], 1.0)  # warm-up
+    runs = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        for w in work:
+            O._single_query(*w, 1.0)
+        runs.append(time.perf_counter() - t0)
+    med = statistics.median(runs)
+    return {
+        "value": n / med, "unit": "tok/s", "cores": threads, "kind": "port",
+        "sample": (f"oracle._single_query fp32 on the first {n} of {cfg.batch} C5 tokens (windows gathered "
+                   f"through the block table, all {cfg.heads_q} heads), median of 3; "
+                   f"{med / n * 1e3:.2f} ms/token"),
+    }
 
 
 def copy_leg(args):
@@ -208,7 +273,9 @@ def main():
         }
         out["roofline"] = {
             "bound": "mfma", "achieved": round(pre["tflops"], 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(pre["tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": None,
+            "frac": round(pre["tflops"] / PEAK_BF16_TFLOPS, 4),
+            "traffic": measured_traffic("prefill_mfma_kernel", args.workload),
+            "algorithmic_bytes": pre["bytes"],
         }
     if "decode" in legs:
         dec = decode_leg(args)
@@ -218,8 +285,7 @@ def main():
             out["unit"] = "tok/s"
             out["ms_per_step"] = round(dec["us_per_step"] / 1e3, 5)
             out["config"] = {"workload": dec["workload"]}
-            out["roofline"] = {"bound": "hbm", "achieved": round(dec["achieved_gbs"], 1), "peak": PEAK_HBM_GBS,
-                               "unit": "GB/s", "frac": round(dec["hbm_frac"], 4), "traffic": None}
+            out["roofline"] = dec["roofline"]
     if "copy" in legs:
         out["copy_calibration"] = copy_leg(args)
     if "cpu" in legs:

@@ -147,25 +147,26 @@ struct RowBlock {
 
   // a_row = bf16(q ⊙ k1_row) for the lane's row; q_neg flips the sign of q
   // (used to keep the softmax scale non-negative).  k1 == nullptr -> zero row.
-  __device__ __forceinline__ void form_a(const bf16* __restrict__ q, const bf16* __restrict__ k1, int half,
-                                         bool q_neg) {
-    if (k1 == nullptr) {
-#pragma unroll
-      for (int t = 0; t < D / 16; ++t) a[t] = bf16x8{};
-      return;
-    }
-    // all 2*D/16 fragment loads are issued before the first use (one memory
-    // round trip); this runs before the accumulators are initialised
+  // A rows of this wave: a_j = bf16(q ⊙ k1_j) for the lane's short-axis key
+  // (zero where `valid` is false).  k1 must point at a readable row in every
+  // lane: the loads are unconditional, so all 2*D/16 fragment loads are in
+  // flight before the first use (one memory round trip).
+  __device__ __forceinline__ void form_a(const bf16* __restrict__ q, const bf16* __restrict__ k1, bool valid,
+                                         int half, bool q_neg) {
+    bf16x8 qv[D / 16], kv[D / 16];
 #pragma unroll
     for (int t = 0; t < D / 16; ++t) {
       const int d0 = 16 * t + 8 * half;
-      const bf16x8 qv = *(const bf16x8*)(q + d0);
-      const bf16x8 kv = *(const bf16x8*)(k1 + d0);
+      qv[t] = *(const bf16x8*)(q + d0);
+      kv[t] = *(const bf16x8*)(k1 + d0);
+    }
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) {
       bf16x8 r;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const float x = (float)qv[u] * (float)kv[u];
-        r[u] = (bf16)(q_neg ? -x : x);
+        const float x = (float)qv[t][u] * (float)kv[t][u];
+        r[u] = valid ? (bf16)(q_neg ? -x : x) : (bf16)0.f;
       }
       a[t] = r;
     }

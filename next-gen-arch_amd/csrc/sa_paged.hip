@@ -76,10 +76,17 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
   const int g = b % p.hk;
   const int token = b / p.hk;
 
-  // per-token scalars (metadata loads are uniform: keep them in SGPRs)
-  const int64_t seq = clamp64(__builtin_amdgcn_readfirstlane((int)load_index(p.tseq, token, p.tok64)), 0,
-                              p.num_seqs - 1);
-  const int pos = __builtin_amdgcn_readfirstlane((int)load_index(p.tpos, token, p.tok64));
+  // per-token scalars, both index loads in one round trip (uniform: SGPRs)
+  int seq_raw, pos_raw;
+  if (p.tok64) {
+    seq_raw = (int)clamp64(((const int64_t*)p.tseq)[token], 0, p.num_seqs - 1);
+    pos_raw = (int)((const int64_t*)p.tpos)[token];
+  } else {
+    seq_raw = min(max(((const int32_t*)p.tseq)[token], 0), p.num_seqs - 1);
+    pos_raw = ((const int32_t*)p.tpos)[token];
+  }
+  const int64_t seq = __builtin_amdgcn_readfirstlane(seq_raw);
+  const int pos = __builtin_amdgcn_readfirstlane(pos_raw);
   const int task = tb * NW + wid;
   const bool task_ok = task < p.tasks;
   const int hi = task_ok ? task % p.group : 0;
@@ -95,12 +102,6 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
   const int cbeg = cfirst + split * per;
   const int cend = min(p.nc, cbeg + per);
 
-  auto row_off = [&](const void* table, int64_t ts, int tw, int64_t nblk, int64_t cb, int64_t cs, int64_t ch,
-                     int ps) -> int64_t {
-    const int64_t blk = block_of(table, p.table64, ts, tw, nblk, seq, ps, p.bs);
-    return blk * cb + (int64_t)(ps % p.bs) * cs + (int64_t)g * ch;
-  };
-
   RowBlock<D> rb;
   const int j = pos - 32 * r - n;
   const bool row_ok = task_ok && j >= lo1 && cbeg < cend;
@@ -110,45 +111,93 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
   // load inside the pipeline would be a vector load whose result feeds a DMA
   // address, and waiting for it would also wait for every older tile load
   // (vector loads complete in order).  The split count guarantees the
-  // split's positions fit (kPosCache).
+  // split's positions fit (kPosCache).  All block-table loads of the
+  // workgroup, including this lane's short-axis row, go out in one round trip.
   int64_t* roff = (int64_t*)(lds + R * SLOT);
   const int ps_lo = max(lo2, kstart + kChunk * cbeg);
   const int ps_hi = min(pos, kstart + kChunk * cend - 1);
-  if (cbeg < cend) {
-    const int npos = min(ps_hi - ps_lo + 1, kPosCache);
-    for (int i = tid; i < npos; i += 64 * NW) {
-      const int ps = ps_lo + i;
-      const int64_t blk = block_of(p.ltable, p.table64, p.lt_s, p.lt_w, p.l_blocks, seq, ps, p.bs);
-      roff[i] = blk * p.lc_b + (int64_t)(ps % p.bs) * p.lc_s + (int64_t)g * p.lc_h;
+  const int npos = cbeg < cend ? min(ps_hi - ps_lo + 1, kPosCache) : 0;
+  // Lookups are branch-free (clamped indices) so that every load of a batch
+  // is in flight before the first result is used.
+  constexpr int kBatch = 4;  // long-axis table loads in flight per lane
+  constexpr int kStep = kBatch * 64 * NW;
+  int64_t soff = 0;
+  auto fill = [&](int i0, bool with_short) {
+    int64_t raw[kBatch], sraw = 0;
+    auto lookup = [&](auto tag) {
+      using I = decltype(tag);
+      const I* lt = (const I*)p.ltable + seq * p.lt_s;
+      const I* st = (const I*)p.stable + seq * p.st_s;
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int ps = ps_lo + min(i0 + tid + u * 64 * NW, npos - 1);
+        raw[u] = (int64_t)lt[min(ps / p.bs, p.lt_w - 1)];
+      }
+      if (with_short) sraw = (int64_t)st[min(max(j, 0) / p.bs, p.st_w - 1)];
+    };
+    if (p.table64) lookup(int64_t{});
+    else lookup(int32_t{});
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int i = i0 + tid + u * 64 * NW;
+      if (i < npos)
+        roff[i] = clamp64(raw[u], 0, p.l_blocks - 1) * p.lc_b + (int64_t)((ps_lo + i) % p.bs) * p.lc_s +
+                  (int64_t)g * p.lc_h;
     }
-    __syncthreads();
+    if (with_short && row_ok)
+      soff = clamp64(sraw, 0, p.s_blocks - 1) * p.sc_b + (int64_t)(j % p.bs) * p.sc_s + (int64_t)g * p.sc_h;
+  };
+  if (npos > 0) {
+    fill(0, true);
+    for (int i0 = kStep; i0 < npos; i0 += kStep) fill(i0, false);
   }
+  __syncthreads();
 
   // this lane's tile row / segment / tensor for each of its DMA instructions
   int drow[NI], dseg[NI], dv[NI];
 #pragma unroll
   for (int k = 0; k < NI; ++k) G::decode(wid, k, lane, dv[k], drow[k], dseg[k]);
 
-  // tile rows outside [lo2, pos] re-read the nearest valid row (masked later)
+  // tile rows outside [lo2, pos] re-read the nearest valid row (masked later);
+  // every row offset is read from LDS before the first DMA is issued
   auto issue = [&](int c) {
     const int k0 = kstart + kChunk * c;
     char* slot = lds + (c % R) * SLOT;
+    constexpr int KG = NI < 8 ? NI : 8;  // offsets read per group of DMA instructions
+    static_for<0, (NI + KG - 1) / KG>([&](auto kg) {
+      constexpr int kb = decltype(kg)::value * KG;
+      int64_t off[KG];
 #pragma unroll
-    for (int k = 0; k < NI; ++k) {
-      const int ps = min(max(k0 + drow[k], lo2), pos);
-      const int64_t off = roff[min(ps - ps_lo, kPosCache - 1)] + (dv[k] ? p.lc_a : 0) + dseg[k] * 8;
-      dma16(p.lc + off, G::dst(slot, wid, k));
-    }
+      for (int k = 0; k < KG; ++k)
+        if (kb + k < NI) off[k] = roff[min(min(max(k0 + drow[kb + k], lo2), pos) - ps_lo, kPosCache - 1)];
+#pragma unroll
+      for (int k = 0; k < KG; ++k)
+        if (kb + k < NI)
+          dma16(p.lc + off[k] + (dv[kb + k] ? p.lc_a : 0) + dseg[kb + k] * 8, G::dst(slot, wid, kb + k));
+    });
   };
 
+  // v1 of this lane's short row, in the layout the epilogue consumes: loaded
+  // with the A-row inputs and held in registers through the key loop (D <= 128;
+  // at D = 256 the registers are needed by the accumulators and the epilogue
+  // loads it)
+  constexpr bool kV1Regs = D <= 128;
+  bf16x4 v1r[kV1Regs ? D / 64 : 1][2][4];
   if (cbeg < cend) {
 #pragma unroll
     for (int e = 0; e < P; ++e)
       if (cbeg + e < cend) issue(cbeg + e);
-    // A rows after the tile loads are in flight: the k1 gathers overlap them
-    const bf16* k1row =
-        row_ok ? p.sc + row_off(p.stable, p.st_s, p.st_w, p.s_blocks, p.sc_b, p.sc_s, p.sc_h, j) : nullptr;
-    rb.form_a(p.q + (int64_t)token * p.q_st + (int64_t)h * p.q_sh, k1row, half, p.q_neg != 0);
+    if constexpr (kV1Regs) {
+      const bf16* v1row = p.sc + soff + p.sc_a;
+#pragma unroll
+      for (int sl = 0; sl < D / 64; ++sl)
+#pragma unroll
+        for (int dbl = 0; dbl < 2; ++dbl)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4)
+            v1r[sl][dbl][q4] = *(const bf16x4*)(v1row + 64 * sl + 32 * dbl + 8 * q4 + 4 * half);
+    }
+    rb.form_a(p.q + (int64_t)token * p.q_st + (int64_t)h * p.q_sh, p.sc + soff, row_ok, half, p.q_neg != 0);
     rb.reset();
     for (int c = cbeg; c < cend; ++c) {
       wait_tiles<NI, P>(min(P - 1, cend - 1 - c));
@@ -162,6 +211,14 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
     }
     block_barrier();
   } else {
+    if constexpr (kV1Regs) {
+#pragma unroll
+      for (int sl = 0; sl < D / 64; ++sl)
+#pragma unroll
+        for (int dbl = 0; dbl < 2; ++dbl)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) v1r[sl][dbl][q4] = bf16x4{};
+    }
     rb.reset();
   }
 
@@ -172,7 +229,6 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
   const float Mw = wave_max(mrow);
   const float wgt = (row_ok && Mw > -INFINITY) ? fast_exp2(mrow - Mw) : 0.f;
   const float Zw = half_sum(wgt * zrow);
-  const bf16* v1row = row_ok ? p.sc + row_off(p.stable, p.st_s, p.st_w, p.s_blocks, p.sc_b, p.sc_s, p.sc_h, j) + p.sc_a : nullptr;
   float* red = (float*)lds + wid * (64 * 36);
   const int pidx = split * p.nr + r;
   const int64_t prow = ((int64_t)pidx * p.tokens + token) * p.hq + h;
@@ -184,7 +240,9 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const int dd = 32 * dbl + 8 * q4 + 4 * half;
-        bf16x4 vv = row_ok ? *(const bf16x4*)(v1row + 64 * sl + dd) : bf16x4{};
+        bf16x4 vv;
+        if constexpr (kV1Regs) vv = row_ok ? v1r[sl][dbl][q4] : bf16x4{};
+        else vv = row_ok ? *(const bf16x4*)(p.sc + soff + p.sc_a + 64 * sl + dd) : bf16x4{};
 #pragma unroll
         for (int e = 0; e < 4; ++e) red[(dd + e) * 36 + n] = wgt * (float)vv[e] * rb.o[db][4 * q4 + e];
       }
@@ -333,7 +391,7 @@ size_t paged_workspace_bytes(const sa_paged_args* a, int splits) {
 }
 
 #ifndef SA_PAGED_DEPTH
-#define SA_PAGED_DEPTH 1
+#define SA_PAGED_DEPTH 2
 #endif
 constexpr int kPagedDepth = SA_PAGED_DEPTH;  // tiles in flight per workgroup (2 workgroups fit one CU)
 

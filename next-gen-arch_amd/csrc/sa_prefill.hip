@@ -170,8 +170,10 @@ __global__ __launch_bounds__(256, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_SIMD)) vo
   for (int r = 0; r < p.nr; ++r) {
     const int j = t - 32 * r - n;  // this lane's short-axis key
     const bool row_ok = qvalid && j >= lo1;
-    rb.form_a(p.q + (int64_t)t * p.q_st + (int64_t)h * p.q_sh,
-              row_ok ? p.k1 + (int64_t)j * k_st + k_g : nullptr, half, p.q_neg != 0);
+    // unconditional loads from clamped (always readable) rows; invalid rows are zeroed
+    const int tc = min(t, last), jc = min(max(j, 0), last);
+    rb.form_a(p.q + (int64_t)tc * p.q_st + (int64_t)h * p.q_sh, p.k1 + (int64_t)jc * k_st + k_g, row_ok, half,
+              p.q_neg != 0);
     rb.reset();
 
 #pragma unroll
