@@ -94,6 +94,16 @@ __device__ __forceinline__ void block_barrier() {
   __builtin_amdgcn_s_barrier();
 }
 
+// A wave-uniform pointer pinned to SGPRs, so that DMA addresses take the
+// scalar-base + 32-bit lane-offset form (no per-lane 64-bit adds).
+template <typename T>
+__device__ __forceinline__ const T* uniform_ptr(const T* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const T*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ void dma16(const void* src, char* dst) {
   __builtin_amdgcn_global_load_lds(src, (lds_void*)dst, 16, 0, 0);
 }
@@ -130,6 +140,18 @@ __device__ __forceinline__ void lds_wait(shortx4& a, shortx4& b) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b));
 }
 
+// Initial running max: finite, so that exp2(s*c - m) of a masked score
+// (s = -inf) is exactly 0 even before a row has seen a valid key; the first
+// valid chunk always triggers a rescale (by exp2(kMInit - m') = 0).
+constexpr float kMInit = -1e30f;
+
+// Two fp32 values rounded to a packed bf16 pair (one v_cvt_pk_bf16_f32).
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  const floatx2 f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+}
+
 // Per-wave state for 32 A rows.
 template <int D>
 struct RowBlock {
@@ -141,34 +163,70 @@ struct RowBlock {
   __device__ __forceinline__ void reset() {
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) o[i] = floatx16{};
-    m = -INFINITY;
+    m = kMInit;
     z = 0.f;
   }
 
-  // a_row = bf16(q ⊙ k1_row) for the lane's row; q_neg flips the sign of q
-  // (used to keep the softmax scale non-negative).  k1 == nullptr -> zero row.
-  // A rows of this wave: a_j = bf16(q ⊙ k1_j) for the lane's short-axis key
-  // (zero where `valid` is false).  k1 must point at a readable row in every
-  // lane: the loads are unconditional, so all 2*D/16 fragment loads are in
-  // flight before the first use (one memory round trip).
-  __device__ __forceinline__ void form_a(const bf16* __restrict__ q, const bf16* __restrict__ k1, bool valid,
-                                         int half, bool q_neg) {
-    bf16x8 qv[D / 16], kv[D / 16];
+  // A rows of this wave: a_j = bf16(q ⊙ k1_j) for the lane's short-axis key,
+  // zero where `valid` is false (q_neg flips the sign of q, which keeps the
+  // softmax scale non-negative).  Split in two so that callers can issue
+  // other loads between the fragment loads and their first use: load_a
+  // reads the 2*D/16 fragments (q and k1 must point at readable rows in
+  // every lane), make_a forms the bf16 products.
+  struct AInputs {
+    bf16x8 q[D / 16], k[D / 16];
+  };
+  __device__ static __forceinline__ AInputs load_a(const bf16* __restrict__ q, const bf16* __restrict__ k1,
+                                                   int half) {
+    AInputs in;
 #pragma unroll
     for (int t = 0; t < D / 16; ++t) {
       const int d0 = 16 * t + 8 * half;
-      qv[t] = *(const bf16x8*)(q + d0);
-      kv[t] = *(const bf16x8*)(k1 + d0);
+      in.q[t] = *(const bf16x8*)(q + d0);
+      in.k[t] = *(const bf16x8*)(k1 + d0);
     }
+    return in;
+  }
+  __device__ __forceinline__ void make_a(const AInputs& in, bool valid, bool q_neg) {
 #pragma unroll
     for (int t = 0; t < D / 16; ++t) {
       bf16x8 r;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const float x = (float)qv[t][u] * (float)kv[t][u];
+        const float x = (float)in.q[t][u] * (float)in.k[t][u];
         r[u] = valid ? (bf16)(q_neg ? -x : x) : (bf16)0.f;
       }
       a[t] = r;
+    }
+  }
+  __device__ __forceinline__ void form_a(const bf16* __restrict__ q, const bf16* __restrict__ k1, bool valid,
+                                         int half, bool q_neg) {
+    make_a(load_a(q, k1, half), valid, q_neg);
+  }
+  // The same from rows staged in LDS: krow = the lane's k1 row, qrow = the
+  // wave's q row (both D contiguous bf16).
+  // Fragments are read in groups of 4 (bounded register footprint).
+  __device__ __forceinline__ void form_a_lds(const char* krow, const char* qrow, bool valid, int half, bool q_neg) {
+    constexpr int GRP = D / 16 < 4 ? D / 16 : 4;
+#pragma unroll
+    for (int t0 = 0; t0 < D / 16; t0 += GRP) {
+      bf16x8 qv[GRP], kv[GRP];
+#pragma unroll
+      for (int u = 0; u < GRP; ++u) {
+        qv[u] = *(const bf16x8*)(qrow + 32 * (t0 + u) + 16 * half);
+        kv[u] = *(const bf16x8*)(krow + 32 * (t0 + u) + 16 * half);
+      }
+#pragma unroll
+      for (int u = 0; u < GRP; ++u) {
+        bf16x8 r;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = (float)qv[u][e] * (float)kv[u][e];
+          r[e] = valid ? (bf16)(q_neg ? -x : x) : (bf16)0.f;
+        }
+        a[t0 + u] = r;
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
@@ -236,25 +294,27 @@ struct RowBlock {
       m = mn;
     }
     float zs = 0.f;
-    bf16x8 pb[2];
+    uint32_t pk[8];
     if (masked) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kr = 8 * (r >> 2) + (r & 3);
-        const bool ok = kr >= lo_h && kr <= hi_h;
-        const float p = ok ? fast_exp2(fmaf(s[r], sl2, -m)) : 0.f;
-        zs += p;
-        pb[r >> 3][r & 7] = (bf16)p;
+      for (int r = 0; r < 16; r += 2) {
+        const int kr0 = 8 * (r >> 2) + (r & 3), kr1 = kr0 + 1;
+        const float p0 = (kr0 >= lo_h && kr0 <= hi_h) ? fast_exp2(fmaf(s[r], sl2, -m)) : 0.f;
+        const float p1 = (kr1 >= lo_h && kr1 <= hi_h) ? fast_exp2(fmaf(s[r + 1], sl2, -m)) : 0.f;
+        zs += p0 + p1;
+        pk[r >> 1] = pack_bf16(p0, p1);
       }
     } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(fmaf(s[r], sl2, -m));
-        zs += p;
-        pb[r >> 3][r & 7] = (bf16)p;
+      for (int r = 0; r < 16; r += 2) {
+        const float p0 = fast_exp2(fmaf(s[r], sl2, -m)), p1 = fast_exp2(fmaf(s[r + 1], sl2, -m));
+        zs += p0 + p1;
+        pk[r >> 1] = pack_bf16(p0, p1);
       }
     }
     z += zs;
+    const bf16x8 pb[2] = {__builtin_bit_cast(bf16x8, u32x4{pk[0], pk[1], pk[2], pk[3]}),
+                          __builtin_bit_cast(bf16x8, u32x4{pk[4], pk[5], pk[6], pk[7]})};
     // V^T operand through the transposing read: within each 16-lane group,
     // source lane (4e + q) fetches 4 consecutive d of row (key e); output lane
     // i then holds d = d0 + i for the 4 keys.  Lane l ends with d = 32*db + l%32
@@ -282,6 +342,138 @@ struct RowBlock {
         v2 = n2;
       }
     });
+  }
+
+  // ---- Software-pipelined form -------------------------------------------
+  // A key chunk is processed in two phases that each pair one group of
+  // MFMAs with VALU work that does not depend on it:
+  //   phase 1: QK^T MFMAs of chunk c+1  ||  probabilities of chunk c
+  //   phase 2: PV MFMAs of chunk c      ||  row maxima of chunk c+1
+  // Scheduling barriers keep the instructions in this order, so the VALU
+  // work of a wave issues while its own MFMAs occupy the matrix core.
+
+  // Raw scores of one chunk (pipeline prologue; no interleaving).
+  template <int RS>
+  __device__ __forceinline__ floatx16 qk(const char* ktile, int row0, int lane) const {
+    const int n = lane & 31, half = lane >> 5;
+    const char* kp = ktile + (row0 + n) * RS + 16 * half;
+    floatx16 s = floatx16{};
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) s = mfma32x32x16(*(const bf16x8*)(kp + 32 * t), a[t], s);
+    return s;
+  }
+
+  // Row maximum of a score tile (both halves), unscaled.
+  __device__ static __forceinline__ float row_max(const floatx16& s) {
+    float r = fmaxf(s[0], s[1]);
+#pragma unroll
+    for (int i = 2; i < 16; i += 2) r = fmaxf(r, fmaxf(s[i], s[i + 1]));
+    return pair_max(r);
+  }
+
+  // Scores of keys outside [key_lo, key_hi] (chunk-relative) become -inf.
+  __device__ static __forceinline__ void mask(floatx16& s, int lane, int key_lo, int key_hi) {
+    const int half = lane >> 5;
+    const int lo_h = key_lo - 4 * half, hi_h = key_hi - 4 * half;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kr = 8 * (r >> 2) + (r & 3);
+      if (kr < lo_h || kr > hi_h) s[r] = -INFINITY;
+    }
+  }
+
+  // Lazy rescale: move the reference max only when a row's scaled max
+  // `cmax` exceeds it by more than 2^8.
+  __device__ __forceinline__ void rescale(float cmax) {
+    const bool grow = cmax > m + 8.0f;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0ull) {
+      const float mn = fmaxf(m, cmax);
+      const float alpha = fast_exp2(m - mn);
+#pragma unroll
+      for (int i = 0; i < D / 32; ++i) o[i] *= alpha;
+      z *= alpha;
+      m = mn;
+    }
+  }
+
+  // One pipelined chunk.  On entry `s` holds chunk c's scores (masked) and
+  // the rescale for chunk c has been applied.  With NEXT, the QK^T of chunk
+  // c+1 (K tile `knext`) is computed into `s` and its scaled row max into
+  // `cmax`.  `vtile` is chunk c's V tile; both tiles use rows row0.. .
+  template <int RS, bool NEXT>
+  __device__ __forceinline__ void step(floatx16& s, float& cmax, const char* knext, const char* vtile, int row0,
+                                       int lane, float sl2) {
+    const int n = lane & 31, half = lane >> 5;
+    constexpr int NT = D / 16;   // QK^T MFMAs
+    constexpr int PER = 16 / NT; // probabilities per QK^T MFMA (2 or 4)
+    floatx16 sn = floatx16{};
+    uint32_t pk[8];              // P^T as packed bf16 pairs (B operand of the PV MFMAs)
+    float zs = 0.f;
+
+    // V^T operand addresses (see vread); the first pair is issued now
+    const int g16 = (lane >> 4) & 1, i16 = lane & 15;
+    const int e_src = i16 >> 2, q_src = i16 & 3;
+    const uint32_t vp = lds_addr(vtile + (row0 + 4 * half + e_src) * RS + 32 * g16 + 8 * q_src);
+    constexpr int kSteps = 2 * (D / 32);
+    shortx4 v1, v2;
+    vread<RS, 0>(vp, v1, v2);
+
+    // phase 1
+    const char* kp = knext + (row0 + n) * RS + 16 * half;
+    bf16x8 kf;
+    if constexpr (NEXT) kf = *(const bf16x8*)kp;
+    static_for<0, NT>([&](auto tt) {
+      constexpr int t = decltype(tt)::value;
+      bf16x8 kn;
+      if constexpr (NEXT) {
+        if constexpr (t + 1 < NT) kn = *(const bf16x8*)(kp + 32 * (t + 1));
+        __builtin_amdgcn_sched_barrier(0);
+        sn = mfma32x32x16(kf, a[t], sn);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < PER; u += 2) {
+        const int r = t * PER + u;
+        const float p0 = fast_exp2(fmaf(s[r], sl2, -m)), p1 = fast_exp2(fmaf(s[r + 1], sl2, -m));
+        zs += p0 + p1;
+        pk[r >> 1] = pack_bf16(p0, p1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (NEXT && t + 1 < NT) kf = kn;
+    });
+    z += zs;
+    const bf16x8 pb0 = __builtin_bit_cast(bf16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
+    const bf16x8 pb1 = __builtin_bit_cast(bf16x8, u32x4{pk[4], pk[5], pk[6], pk[7]});
+
+    // phase 2
+    constexpr int MPER = 16 / kSteps;  // score elements folded into the max per PV MFMA
+    float rmax = -INFINITY;
+    lds_wait(v1, v2);
+    static_for<0, kSteps>([&](auto st) {
+      constexpr int step = decltype(st)::value;
+      shortx8 vv = {v1[0], v1[1], v1[2], v1[3], v2[0], v2[1], v2[2], v2[3]};
+      const bf16x8 vf = __builtin_bit_cast(bf16x8, vv);
+      shortx4 n1, n2;
+      if constexpr (step + 1 < kSteps) vread<RS, step + 1>(vp, n1, n2);
+      __builtin_amdgcn_sched_barrier(0);
+      o[step % (D / 32)] = mfma32x32x16(vf, step / (D / 32) == 0 ? pb0 : pb1, o[step % (D / 32)]);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (NEXT) {
+#pragma unroll
+        for (int u = 0; u < MPER; u += 2)
+          rmax = fmaxf(rmax, fmaxf(sn[step * MPER + u], sn[step * MPER + u + 1]));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (step + 1 < kSteps) {
+        lds_wait(n1, n2);
+        v1 = n1;
+        v2 = n2;
+      }
+    });
+    if constexpr (NEXT) {
+      cmax = pair_max(rmax) * sl2;
+      s = sn;
+    }
   }
 };
 

@@ -247,7 +247,7 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
         for (int e = 0; e < 4; ++e) red[(dd + e) * 36 + n] = wgt * (float)vv[e] * rb.o[db][4 * q4 + e];
       }
     }
-    block_barrier();
+    // `red` is private to this wave and a wave's LDS accesses execute in order
     float acc = 0.f;
     const floatx4* row4 = (const floatx4*)(red + lane * 36);
 #pragma unroll
@@ -255,7 +255,6 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
       floatx4 x = row4[i];
       acc += (x[0] + x[1]) + (x[2] + x[3]);
     }
-    block_barrier();
     if (task_ok) {
       if (p.direct) p.out[(int64_t)token * p.o_st + (int64_t)h * p.o_sh + 64 * sl + lane] = acc / Zw;
       else p.part_o[prow * D + 64 * sl + lane] = acc;
@@ -455,7 +454,7 @@ hipError_t launch_paged(const sa_paged_args* a, int splits, void* ws, size_t ws_
     p.wl = a->long_window;
     p.nc = (int)(((int64_t)a->long_window + kChunk - 1) / kChunk);
     p.nr = (a->short_window + 31) / 32;
-    p.sl2 = fabsf(a->scale) * kLog2e;
+    p.sl2 = fmaxf(fabsf(a->scale) * kLog2e, 1e-30f);  // > 0: a masked score (-inf) maps to p = 0
     p.q_neg = a->scale < 0.f;
     p.splits = splits;
     p.tasks = p.group * p.nr;

@@ -77,7 +77,7 @@ __device__ __forceinline__ int xcd_remap(int b, int n) {
 #define SA_PREFILL_WAVES_PER_SIMD 2
 #endif
 #ifndef SA_PREFILL_DEPTH
-#define SA_PREFILL_DEPTH 3
+#define SA_PREFILL_DEPTH 2
 #endif
 
 template <int D, int NQ, int NH, int P>
@@ -87,9 +87,16 @@ __global__ __launch_bounds__(256, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_SIMD)) vo
   constexpr int NW = 4;
   constexpr int ROWS = kChunk + NQ - 1;  // tile rows: one chunk of all NQ queries
   using G = TileGeom<D, ROWS, NW>;
-  constexpr int R = P + 1;
+  constexpr int R = P + 1;  // ring slots for the long-axis tiles
   constexpr int NI = G::NI;
+  // the pipelined loop holds a second score tile: registers allow it up to D = 128
+  constexpr bool kPipelined = D <= 128 && P >= 2;
   extern __shared__ __attribute__((aligned(16))) char lds[];
+  // One more slot after the ring holds the short window of the pass: its K
+  // region takes the k1 rows and (in its V region) the q rows of the 4 waves
+  // at the start of the pass; the v1 rows replace the q rows during the last
+  // chunk.  All of it arrives by DMA, 1 KB per instruction.
+  char* const sslot = lds + R * G::SLOT;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -138,22 +145,48 @@ __global__ __launch_bounds__(256, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_SIMD)) vo
     G::decode(wid, k, lane, is_v, row, seg);
     voff[k] = (uint32_t)(((int64_t)row * (is_v ? v_st : k_st) + seg * 8) * 2);
   }
-  auto issue = [&](int c) {
-    char* slot = lds + (c % R) * G::SLOT;
-    const int kb = __builtin_amdgcn_readfirstlane(kb0 + kChunk * c);  // uniform: scalar test and tile bases
+  // DMA of one tile of rows kb .. kb+ROWS-1 into `slot`: the K region from
+  // tensor kt (k strides), the V region from vt (v strides).  PART selects
+  // both regions (0), the K region only (1) or the V region only (2).
+  auto dma_tile = [&](auto part_c, char* slot, int kb_in, const bf16* kt, const bf16* vt) {
+    constexpr int PART = decltype(part_c)::value;
+    const int kb = __builtin_amdgcn_readfirstlane(kb_in);  // uniform: scalar test and tile bases
     if (kb >= 0 && kb + ROWS - 1 <= last) {
-      const char* kbase = (const char*)(p.k2 + (int64_t)kb * k_st + k_g);
-      const char* vbase = (const char*)(p.v2 + (int64_t)kb * v_st + v_g);
+      const char* kbase = (const char*)(kt + (int64_t)kb * k_st + k_g);
+      const char* vbase = (const char*)(vt + (int64_t)kb * v_st + v_g);
 #pragma unroll
-      for (int k = 0; k < NI; ++k) dma16((G::instr_is_v(wid, k) ? vbase : kbase) + voff[k], G::dst(slot, wid, k));
+      for (int k = 0; k < NI; ++k) {
+        const bool is_v = G::instr_is_v(wid, k);
+        if ((PART == 1 && is_v) || (PART == 2 && !is_v)) continue;
+        dma16(uniform_ptr(is_v ? vbase : kbase) + voff[k], G::dst(slot, wid, k));
+      }
     } else {  // tile crosses the tensor edge: clamp every row into [0, total)
 #pragma unroll
       for (int k = 0; k < NI; ++k) {
         int is_v, row, seg;
         G::decode(wid, k, lane, is_v, row, seg);
+        if ((PART == 1 && G::instr_is_v(wid, k)) || (PART == 2 && !G::instr_is_v(wid, k))) continue;
         const int64_t key = min(max(kb + row, 0), last);
-        const bf16* src = is_v ? p.v2 + key * v_st + v_g : p.k2 + key * k_st + k_g;
+        const bf16* src = is_v ? vt + key * v_st + v_g : kt + key * k_st + k_g;
         dma16(src + seg * 8, G::dst(slot, wid, k));
+      }
+    }
+  };
+  auto issue = [&](int c) {
+    dma_tile(std::integral_constant<int, 0>{}, lds + (c % R) * G::SLOT, kb0 + kChunk * c, p.k2, p.v2);
+  };
+  // q rows of the 4 waves into rows 0..3 of the short slot's V region (wave 0)
+  auto dma_q = [&]() {
+    if (wid == 0) {
+      constexpr int QI = (4 * G::RS + 1023) / 1024;
+#pragma unroll
+      for (int k = 0; k < QI; ++k) {
+        const int b = k * 1024 + lane * 16;
+        int row = b / G::RS, seg = (b % G::RS) >> 4;
+        if (row >= 4 || seg >= G::kSegs) row = 0, seg = 0;
+        const int tq = min(t0 + row / NH, last);
+        const int hq = g * p.group + hs * NH + row % NH;
+        dma16(p.q + (int64_t)tq * p.q_st + (int64_t)hq * p.q_sh + seg * 8, sslot + G::VOFF + k * 1024);
       }
     }
   };
@@ -170,30 +203,76 @@ __global__ __launch_bounds__(256, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_SIMD)) vo
   for (int r = 0; r < p.nr; ++r) {
     const int j = t - 32 * r - n;  // this lane's short-axis key
     const bool row_ok = qvalid && j >= lo1;
-    // unconditional loads from clamped (always readable) rows; invalid rows are zeroed
-    const int tc = min(t, last), jc = min(max(j, 0), last);
-    rb.form_a(p.q + (int64_t)tc * p.q_st + (int64_t)h * p.q_sh, p.k1 + (int64_t)jc * k_st + k_g, row_ok, half,
-              p.q_neg != 0);
-    rb.reset();
-
+    // Pass prologue: the short window (k1 rows, q rows) and the first P tiles
+    // go out together; A is formed once the short window has landed.
+    const int kbs = t0 - 31 - 32 * r;  // short-slot row 0 (short key of tile row 0)
+    dma_tile(std::integral_constant<int, 1>{}, sslot, kbs, p.k1, p.v1);
+    dma_q();
 #pragma unroll
-    for (int e = 0; e < P; ++e)
-      if (c0 + e < p.nc) issue(c0 + e);
-    for (int c = c0; c < p.nc; ++c) {
-      wait_tiles<NI, P>(min(P - 1, p.nc - 1 - c));
-      block_barrier();  // tile c complete for every wave; slot of tile c-1 free
-      if (c + P < p.nc) issue(c + P);
-      // Unconditional: a wave without valid keys in this step gets an empty
-      // key range (every p = 0, an exact no-op).  A branch here would give
-      // the accumulators two incoming values at the loop latch, which the
-      // register allocator resolves by keeping a second copy of all of O.
-      const bool active = qvalid && c >= cfirst;
-      const int kfirst = t - p.wl + 1 + kChunk * c;  // key of this wave's chunk row 0
-      const char* slot = lds + (c % R) * G::SLOT;
-      rb.template chunk<G::RS>(slot, slot + G::VOFF, qo, lane, p.sl2, active ? max(lo2 - kfirst, 0) : kChunk,
-                               active ? min(t - kfirst, kChunk - 1) : -1);
+    for (int e = 0; e < P; ++e) issue(c0 + e);  // unconditional: static count for the wait below
+    wait_vmcnt<P * NI>();
+    block_barrier();
+    const int srow = qo + 31 - n;  // this lane's short key j in the short slot
+    rb.form_a_lds(sslot + srow * G::RS, sslot + G::VOFF + wid * G::RS, row_ok, half, p.q_neg != 0);
+    rb.reset();
+    if constexpr (kPipelined) {
+      // Software-pipelined chunk loop: iteration c needs K of chunk c+1 and
+      // V of chunk c, so it waits for tile c+1; the slot refilled after the
+      // barrier is the one of tile c-1, whose reads ended in iteration c-1.
+      if (c0 < p.nc) {
+        wait_tiles<NI, P>(min(P - 1, p.nc - 1 - c0));
+        block_barrier();
+        floatx16 s = rb.template qk<G::RS>(lds + (c0 % R) * G::SLOT, qo, lane);
+        float cmax = RowBlock<D>::row_max(s) * p.sl2;
+        // the last chunk (no successor) is peeled off so that the loop body
+        // has a single definition of the accumulators
+        auto begin_chunk = [&](int c, floatx16& sc, float& cm) {
+          block_barrier();
+          if (c + P < p.nc) issue(c + P);
+          const bool active = qvalid && c >= cfirst;
+          const int kfirst = t - p.wl + 1 + kChunk * c;  // key of this wave's chunk row 0
+          const int klo = active ? max(lo2 - kfirst, 0) : kChunk;
+          const int khi = active ? min(t - kfirst, kChunk - 1) : -1;
+          if (klo > 0 || khi < kChunk - 1) {  // edge chunk (uniform branch)
+            RowBlock<D>::mask(sc, lane, klo, khi);
+            cm = RowBlock<D>::row_max(sc) * p.sl2;
+          }
+          rb.rescale(cm);
+        };
+        int c = c0;
+        for (; c + 1 < p.nc; ++c) {
+          wait_tiles<NI, P>(min(P - 2, p.nc - 2 - c));
+          begin_chunk(c, s, cmax);
+          const char* slot = lds + (c % R) * G::SLOT;
+          rb.template step<G::RS, true>(s, cmax, lds + ((c + 1) % R) * G::SLOT, slot + G::VOFF, qo, lane, p.sl2);
+        }
+        begin_chunk(c, s, cmax);
+        dma_tile(std::integral_constant<int, 2>{}, sslot, kbs, p.k1, p.v1);  // v1 rows for the epilogue
+        const char* slot = lds + (c % R) * G::SLOT;
+        rb.template step<G::RS, false>(s, cmax, slot, slot + G::VOFF, qo, lane, p.sl2);
+      } else {
+        dma_tile(std::integral_constant<int, 2>{}, sslot, kbs, p.k1, p.v1);
+      }
+    } else {
+      for (int c = c0; c < p.nc; ++c) {
+        wait_tiles<NI, P>(min(P - 1, p.nc - 1 - c));
+        block_barrier();  // tile c complete for every wave; slot of tile c-1 free
+        if (c + P < p.nc) issue(c + P);
+        if (c + 1 == p.nc) dma_tile(std::integral_constant<int, 2>{}, sslot, kbs, p.k1, p.v1);  // v1 rows
+        // Unconditional: a wave without valid keys in this step gets an empty
+        // key range (every p = 0, an exact no-op).  A branch here would give
+        // the accumulators two incoming values at the loop latch, which the
+        // register allocator resolves by keeping a second copy of all of O.
+        const bool active = qvalid && c >= cfirst;
+        const int kfirst = t - p.wl + 1 + kChunk * c;  // key of this wave's chunk row 0
+        const char* slot = lds + (c % R) * G::SLOT;
+        rb.template chunk<G::RS>(slot, slot + G::VOFF, qo, lane, p.sl2, active ? max(lo2 - kfirst, 0) : kChunk,
+                                 active ? min(t - kfirst, kChunk - 1) : -1);
+      }
+      if (c0 >= p.nc) dma_tile(std::integral_constant<int, 2>{}, sslot, kbs, p.k1, p.v1);
     }
-    block_barrier();  // ring reads done: LDS reused below
+    wait_vmcnt<0>();  // this wave's part of the v1 rows
+    block_barrier();  // ring reads done (LDS reused below); v1 rows complete
 
     // ---- epilogue of this pass: merge the 32 rows of the wave
     const float zrow = pair_sum(rb.z);
@@ -201,8 +280,8 @@ __global__ __launch_bounds__(256, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_SIMD)) vo
     const float Mw = wave_max(mrow);
     const float wgt = (row_ok && Mw > -INFINITY) ? fast_exp2(mrow - Mw) : 0.f;
     const float Zw = half_sum(wgt * zrow);
-    float* red = (float*)lds + wid * (64 * 36);  // [64 d][36] per wave
-    const bf16* v1row = p.v1 + (int64_t)(row_ok ? j : 0) * v_st + v_g;
+    float* red = (float*)lds + wid * (64 * 36);  // [64 d][36] per wave (ring region)
+    const char* v1s = sslot + G::VOFF + srow * G::RS;  // this lane's v1 row
     const float Mn = fmaxf(Mrun, Mw);
     const float a0 = Mrun > -INFINITY ? fast_exp2(Mrun - Mn) : 0.f;
     const float a1 = Mw > -INFINITY ? fast_exp2(Mw - Mn) : 0.f;
@@ -214,12 +293,13 @@ __global__ __launch_bounds__(256, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_SIMD)) vo
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
           const int dd = 32 * dbl + 8 * q4 + 4 * half;  // first of 4 consecutive d
-          bf16x4 vv = row_ok ? *(const bf16x4*)(v1row + 64 * sl + dd) : bf16x4{};
+          const bf16x4 vv = row_ok ? *(const bf16x4*)(v1s + 2 * (64 * sl + dd)) : bf16x4{};
 #pragma unroll
           for (int e = 0; e < 4; ++e) red[(dd + e) * 36 + n] = wgt * (float)vv[e] * rb.o[db][4 * q4 + e];
         }
       }
-      block_barrier();
+      // `red` is private to this wave and a wave's LDS accesses execute in
+      // order: no barrier between the writes above and the reads below
       float acc = 0.f;
       const floatx4* row4 = (const floatx4*)(red + lane * 36);
 #pragma unroll
@@ -227,11 +307,11 @@ __global__ __launch_bounds__(256, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_SIMD)) vo
         floatx4 x = row4[i];
         acc += (x[0] + x[1]) + (x[2] + x[3]);
       }
-      block_barrier();
       orun[sl] = orun[sl] * a0 + acc * a1;
     }
     Zrun = Zrun * a0 + Zw * a1;
     Mrun = Mn;
+    if (r + 1 < p.nr) block_barrier();  // every wave's `red` reads done before the next pass refills the ring
   }
 
   if (qvalid) {
@@ -268,7 +348,7 @@ static hipError_t launch_prefill_mfma(const PrefillParams& base_p, hipStream_t s
   p.hsub = p.group / NH;
   p.nblocks = p.qblocks * p.hk * p.hsub;
   using G = TileGeom<D, kChunk + NQ - 1, 4>;
-  size_t lds = (size_t)(P + 1) * G::SLOT;
+  size_t lds = (size_t)(P + 2) * G::SLOT;  // P + 1 ring slots + the short-window slot
   const size_t red = (size_t)4 * 64 * 36 * sizeof(float);
   if (lds < red) lds = red;
   auto kern = prefill_mfma_kernel<D, NQ, NH, P>;
@@ -324,7 +404,8 @@ hipError_t launch_prefill_bf16_mfma(const sa_prefill_args* a, hipStream_t stream
   p.wl = a->long_window;
   p.nc = (a->long_window + kChunk - 1) / kChunk;
   p.nr = (a->short_window + 31) / 32;
-  p.sl2 = fabsf(a->scale) * kLog2e;
+  // > 0 even for scale == 0, so that a masked score (-inf) maps to p = 0
+  p.sl2 = fmaxf(fabsf(a->scale) * kLog2e, 1e-30f);
   p.q_neg = a->scale < 0.f;
   switch (a->head_dim) {
     case 64: return dispatch_prefill_mfma_d<64>(p, stream);
