@@ -60,6 +60,7 @@ constexpr int kPosCache = 1024;  // long-window positions of one split whose row
 template <int D, int NW, int P>
 __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel(PagedParams p) {
   using G = TileGeom<D, kChunk, NW>;
+  constexpr bool kPipelined = D <= 128 && P >= 2;  // second score tile fits the registers up to D = 128
   constexpr int SLOT = G::SLOT;
   constexpr int R = P + 1;
   constexpr int NI = G::NI;  // DMA instructions per wave per tile
@@ -199,15 +200,46 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
     }
     rb.form_a(p.q + (int64_t)token * p.q_st + (int64_t)h * p.q_sh, p.sc + soff, row_ok, half, p.q_neg != 0);
     rb.reset();
-    for (int c = cbeg; c < cend; ++c) {
-      wait_tiles<NI, P>(min(P - 1, cend - 1 - c));
+    if constexpr (kPipelined) {
+      // software-pipelined loop (see the prefill kernel): iteration c needs K
+      // of chunk c+1 and V of chunk c
+      wait_tiles<NI, P>(min(P - 1, cend - 1 - cbeg));
       block_barrier();
-      if (c + P < cend) issue(c + P);
-      // unconditional (see the prefill kernel): idle waves get an empty key range
-      const int kfirst = kstart + kChunk * c;
+      floatx16 s = rb.template qk<G::RS>(lds + (cbeg % R) * SLOT, 0, lane);
+      float cmax = RowBlock<D>::row_max(s) * p.sl2;
+      auto begin_chunk = [&](int c) {
+        block_barrier();
+        if (c + P < cend) issue(c + P);
+        const int kfirst = kstart + kChunk * c;
+        const int klo = task_ok ? max(lo2 - kfirst, 0) : kChunk;
+        const int khi = task_ok ? min(pos - kfirst, kChunk - 1) : -1;
+        if (klo > 0 || khi < kChunk - 1) {  // edge chunk (uniform branch)
+          RowBlock<D>::mask(s, lane, klo, khi);
+          cmax = RowBlock<D>::row_max(s) * p.sl2;
+        }
+        rb.rescale(cmax);
+      };
+      int c = cbeg;
+      for (; c + 1 < cend; ++c) {
+        wait_tiles<NI, P>(min(P - 2, cend - 2 - c));
+        begin_chunk(c);
+        const char* slot = lds + (c % R) * SLOT;
+        rb.template step<G::RS, true>(s, cmax, lds + ((c + 1) % R) * SLOT, slot + G::VOFF, 0, lane, p.sl2);
+      }
+      begin_chunk(c);
       const char* slot = lds + (c % R) * SLOT;
-      rb.template chunk<G::RS>(slot, slot + G::VOFF, 0, lane, p.sl2, task_ok ? max(lo2 - kfirst, 0) : kChunk,
-                               task_ok ? min(pos - kfirst, kChunk - 1) : -1);
+      rb.template step<G::RS, false>(s, cmax, slot, slot + G::VOFF, 0, lane, p.sl2);
+    } else {
+      for (int c = cbeg; c < cend; ++c) {
+        wait_tiles<NI, P>(min(P - 1, cend - 1 - c));
+        block_barrier();
+        if (c + P < cend) issue(c + P);
+        // unconditional (see the prefill kernel): idle waves get an empty key range
+        const int kfirst = kstart + kChunk * c;
+        const char* slot = lds + (c % R) * SLOT;
+        rb.template chunk<G::RS>(slot, slot + G::VOFF, 0, lane, p.sl2, task_ok ? max(lo2 - kfirst, 0) : kChunk,
+                                 task_ok ? min(pos - kfirst, kChunk - 1) : -1);
+      }
     }
     block_barrier();
   } else {
