@@ -1,0 +1,117 @@
+"""Drop-ins with the signatures of the reference's TileLang entry points
+(``archlab.architectures.tilelang_attention``: ``tilelang_attention``
+:341-380 and ``tilelang_decode`` :383-420), running on this library's
+kernels instead of TileLang.
+
+``tilelang_attention(q, k, v, *, scaling, long_window, short=None, ...)``:
+with ``short=(k1, v1)`` the joint 2-simplicial softmax over the short axis
+(k1, v1, ``min(short_window, long_window)``, at most 16) and the long axis
+(k, v, ``long_window``); without ``short`` ordinary causal sliding-window
+attention over (k, v), evaluated as the 2-simplicial form with k1 = v1 = 1
+and a short window of one key (the score reduces to q·k exactly).  Output is
+fp32 [B, N, H, D], as the reference returns; the bf16 kernel's output is
+widened.  ``dynamic_length`` and ``shared_gradient_dtype`` only select
+reference compilation / backward variants and do not change the forward.
+
+``tilelang_decode(q, k, v, *, scaling, short=None, lengths=None,
+query_position=None, long_window=None)``: one query per batch row against
+the cached rows: every short row (at most 16) with every long row in
+``[key_lower, N2)`` (aligned local decode trims the history exactly as the
+reference does), or, with ``lengths = [long length, short length, start]``,
+the long rows ``[start, start + long length)`` and the last ``short length``
+short rows.  fp32 [B, 1, H, D].
+
+Deviations: forward only (no backward kernel); allowed under deterministic
+mode; the bounded form reads ``lengths`` on the host (one synchronisation),
+where the reference reads it in the kernel.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .simplicial_attention import simplicial_attention
+from .window_decode import window_decode
+
+
+def _validate(q, k, v, short):
+    inputs = (q, k, v, *(short or ()))
+    if any(x.ndim != 4 for x in inputs):
+        raise ValueError("expected [batch, sequence, heads, head_dim]")
+    if not q.is_cuda or any(x.device != q.device or x.dtype != torch.bfloat16 for x in inputs):
+        raise ValueError("TileLang attention requires CUDA BF16 inputs")
+    if q.shape[-1] != 128 or min(q.shape) < 1 or min(k.shape) < 1:
+        raise ValueError("TileLang attention requires nonempty native head_dim=128")
+    if (
+        k.shape != v.shape
+        or k.shape[0] != q.shape[0]
+        or k.shape[-1] != q.shape[-1]
+        or q.shape[2] % k.shape[2]
+    ):
+        raise ValueError("incompatible grouped-query geometry")
+    if short and (
+        short[0].shape != short[1].shape
+        or short[0].shape[0] != q.shape[0]
+        or short[0].shape[2:] != k.shape[2:]
+    ):
+        raise ValueError("incompatible short-axis geometry")
+
+
+def tilelang_attention(q, k, v, *, scaling, long_window, short=None, short_window=1, normal_kernel="shared",
+                       dynamic_length=False, shared_gradient_dtype=torch.float32):
+    _validate(q, k, v, short)
+    if not math.isfinite(scaling) or scaling <= 0 or long_window < 1 or not 1 <= short_window <= 16:
+        raise ValueError("invalid attention scale/window")
+    if k.shape[1] != q.shape[1] or (short and short[0].shape[1] != q.shape[1]):
+        raise ValueError("training attention requires matching sequence lengths")
+    if normal_kernel not in ("shared", "gqa"):
+        raise ValueError("normal_kernel must be shared or gqa")
+    if shared_gradient_dtype not in (torch.float32, torch.float64):
+        raise ValueError("shared gradient accumulation requires FP32 or FP64")
+    if short is None and normal_kernel == "gqa" and shared_gradient_dtype != torch.float32:
+        raise ValueError("wide shared gradient accumulation requires the shared kernel")
+    if short:
+        k1, v1 = short
+        w_short = min(short_window, long_window)
+    else:
+        k1 = torch.ones_like(k)
+        v1 = torch.ones_like(v)
+        w_short = 1
+    out = simplicial_attention(q, k1, k, v1, v, w_short, long_window, scale=float(scaling))
+    return out.float()
+
+
+def tilelang_decode(q, k, v, *, scaling, short=None, lengths=None, query_position=None, long_window=None):
+    _validate(q, k, v, short)
+    if q.shape[1] != 1 or torch.is_grad_enabled():
+        raise ValueError("cached TileLang decode requires one token without gradients")
+    key_lower = 0
+    if query_position is not None or long_window is not None:
+        if (short is None or lengths is not None or type(query_position) is not int
+                or query_position < 0 or type(long_window) is not int or long_window < 1):
+            raise ValueError("aligned local decode requires a position, window and simplicial history")
+        start = max(0, query_position // 4 * 4 - long_window + 1)
+        required = query_position + 1 - start
+        if k.shape[1] < required:
+            raise ValueError("aligned local decode lacks its masked query-group history")
+        k, v = k[:, -required:], v[:, -required:]
+        key_lower = max(0, query_position - long_window + 1) - start
+    if short:
+        k1, v1 = short
+    else:
+        k1 = torch.ones_like(k[:, :1])
+        v1 = torch.ones_like(v[:, :1])
+    s = 16 if short else 1
+    w1 = k1.shape[1] if short else 1
+    if not 1 <= w1 <= s:
+        raise ValueError("cached short axis exceeds 16 keys")
+    if lengths is not None:
+        long_len, short_len, start = (int(x) for x in lengths.tolist()[:3])
+        k, v = k[:, start:start + long_len], v[:, start:start + long_len]
+        if short:
+            keep = max(0, min(short_len, s, k1.shape[1]))
+            k1, v1 = k1[:, k1.shape[1] - keep:], v1[:, v1.shape[1] - keep:]
+    out = window_decode(q[:, 0], k1, k, v1, v, float(scaling), key_lower=key_lower)
+    return out[:, None]

@@ -1,0 +1,176 @@
+"""GPU parity of the reference's other entry points that compute the same
+attention: the contiguous one-token decodes (simplicial_decode.py:47-72,
+simplicial_packed.py:290-338), the packed fp32 prefill (simplicial_packed.py:
+227-235), the deterministic form (simplicial_deterministic.py:107-111) and
+the TileLang signatures (tilelang_attention.py:341-420).
+
+Each is checked against the CPU oracle on the same seeded values: a decode
+query attends to every pair of its explicit windows (oracle
+``_single_query``), the prefill forms to their causal windows
+(``reference_simplicial``).  Tolerances: fp32 1e-4; bf16 out max-abs 2e-2.
+"""
+
+import math
+
+import pytest
+import torch
+
+from helpers import assert_out_close, rand_inputs
+from oracle import simplicial_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _windows(b, hq, hk, d, n1, n2, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, 1, hq, d, generator=g) / math.sqrt(d)
+    k1, v1 = (torch.randn(b, n1, hk, d, generator=g) for _ in range(2))
+    k2, v2 = (torch.randn(b, n2, hk, d, generator=g) for _ in range(2))
+    return [x.to(dtype) for x in (q, k1, k2, v1, v2)]
+
+
+def _decode_ref(q, k1, k2, v1, v2, scale):
+    outs = []
+    for i in range(q.shape[0]):
+        o, _ = O._single_query(q[i, 0].double(), k1[i].double(), k2[i].double(), v1[i].double(),
+                               v2[i].double(), scale)
+        outs.append(o)
+    return torch.stack(outs)[:, None].float()
+
+
+@pytest.mark.parametrize("hq,hk,d,n1,n2", [(8, 2, 64, 5, 37), (4, 4, 128, 16, 300), (6, 3, 32, 1, 1),
+                                           (16, 4, 256, 9, 129)])
+def test_simplicial_decode_attention(cuda, hq, hk, d, n1, n2):
+    from archlab_amd import simplicial_decode_attention
+    x = _windows(3, hq, hk, d, n1, n2, torch.float32, seed=n2)
+    out = simplicial_decode_attention(*(t.to(cuda) for t in x))
+    assert out.shape == x[0].shape and out.dtype == torch.float32
+    ref = _decode_ref(*x, d ** -0.5)
+    print(f"decode h{hq}/{hk} d{d} n1={n1} n2={n2}: {(out.cpu() - ref).abs().max().item():.2e}")
+    assert_out_close(out, ref, torch.float32)
+
+
+@pytest.mark.parametrize("n1,n2", [(16, 16), (3, 200), (16, 1000)])
+def test_packed_simplicial_decode(cuda, n1, n2):
+    from archlab_amd import packed_simplicial_decode
+    x = _windows(2, 8, 2, 128, n1, n2, torch.float32, seed=7)
+    out = packed_simplicial_decode(*(t.to(cuda) for t in x))
+    assert_out_close(out, _decode_ref(*x, 128 ** -0.5), torch.float32)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_packed_simplicial_attention(cuda, dtype):
+    from archlab_amd import packed_simplicial_attention
+    x = rand_inputs(2, 70, 8, 2, 128, seed=3, dtype=dtype)
+    out = packed_simplicial_attention(*(t.to(cuda) for t in x), 7, 40)
+    assert out.dtype == torch.float32 and out.shape == x[0].shape
+    ref = O.reference_simplicial(*(t.float() for t in x), 7, 40, scale=128 ** -0.5)
+    # fp32 arithmetic on the (possibly bf16-valued) inputs, as the reference's fp32 forward buffers
+    assert_out_close(out, ref, torch.float32)
+
+
+def test_packed_simplicial_attention_mixed_query(cuda):
+    """fp32 query with bf16 keys/values (allow_scaled_query)."""
+    from archlab_amd import packed_simplicial_attention
+    x = rand_inputs(1, 33, 4, 4, 128, seed=5, dtype=torch.bfloat16)
+    x[0] = x[0].float() * 1.7
+    out = packed_simplicial_attention(*(t.to(cuda) for t in x), 16, 20)
+    ref = O.reference_simplicial(*(t.float() for t in x), 16, 20, scale=128 ** -0.5)
+    assert_out_close(out, ref, torch.float32)
+
+
+def test_deterministic_simplicial_attention(cuda):
+    from archlab_amd import deterministic_simplicial_attention
+    x = rand_inputs(1, 45, 6, 3, 64, seed=11, dtype=torch.float32)
+    with_det = torch.are_deterministic_algorithms_enabled()
+    torch.use_deterministic_algorithms(True)
+    try:
+        a = deterministic_simplicial_attention(*(t.to(cuda) for t in x), 5, 17)
+        b = deterministic_simplicial_attention(*(t.to(cuda) for t in x), 5, 17)
+    finally:
+        torch.use_deterministic_algorithms(with_det)
+    assert torch.equal(a, b)
+    assert_out_close(a, O.reference_simplicial(*x, 5, 17), torch.float32)
+
+
+def _band_attention(q, k, v, window, scale):
+    """Ordinary causal sliding-window softmax attention (fp32, CPU)."""
+    b, n, hq, d = q.shape
+    g = hq // k.shape[2]
+    k, v = (x.repeat_interleave(g, dim=2) for x in (k, v))
+    s = torch.einsum("bihd,bjhd->bhij", q.double(), k.double()) * scale
+    i = torch.arange(n)[:, None]
+    j = torch.arange(n)[None, :]
+    s = s.masked_fill(~((j <= i) & (j > i - window)), float("-inf"))
+    return torch.einsum("bhij,bjhd->bihd", s.softmax(-1), v.double()).float()
+
+
+@pytest.mark.parametrize("window,short_window", [(64, 16), (500, 3)])
+def test_tilelang_attention_joint(cuda, window, short_window):
+    from archlab_amd import tilelang_attention
+    q, k1, k, v1, v = rand_inputs(2, 150, 8, 2, 128, seed=window, dtype=torch.bfloat16)
+    out = tilelang_attention(q.to(cuda), k.to(cuda), v.to(cuda), scaling=0.7, long_window=window,
+                             short=(k1.to(cuda), v1.to(cuda)), short_window=short_window)
+    assert out.dtype == torch.float32 and out.shape == q.shape
+    ref = O.reference_simplicial(*(t.float() for t in (q, k1, k, v1, v)), min(short_window, window), window,
+                                 scale=0.7)
+    assert_out_close(out, ref, torch.bfloat16)
+
+
+def test_tilelang_attention_ordinary(cuda):
+    from archlab_amd import tilelang_attention
+    q, _, k, _, v = rand_inputs(1, 130, 8, 4, 128, seed=2, dtype=torch.bfloat16)
+    out = tilelang_attention(q.to(cuda), k.to(cuda), v.to(cuda), scaling=128 ** -0.5, long_window=40)
+    ref = _band_attention(q.float(), k.float(), v.float(), 40, 128 ** -0.5)
+    assert_out_close(out, ref, torch.bfloat16)
+
+
+def test_tilelang_decode_forms(cuda):
+    from archlab_amd import tilelang_decode
+    b, hq, hk, d, n1, n2 = 2, 8, 2, 128, 16, 300
+    q, k1, k, v1, v = _windows(b, hq, hk, d, n1, n2, torch.bfloat16, seed=9)
+    dev = [t.to(cuda) for t in (q, k1, k, v1, v)]
+    f = lambda t: t.float()  # noqa: E731
+    # joint decode over every cached row
+    with torch.no_grad():
+        out = tilelang_decode(dev[0], dev[2], dev[4], scaling=0.5, short=(dev[1], dev[3]))
+    assert out.dtype == torch.float32 and out.shape == q.shape
+    assert_out_close(out, _decode_ref(f(q), f(k1), f(k), f(v1), f(v), 0.5), torch.bfloat16)
+    # ordinary decode (no short axis)
+    with torch.no_grad():
+        out = tilelang_decode(dev[0], dev[2], dev[4], scaling=0.5)
+    ones = torch.ones(b, 1, hk, d)
+    assert_out_close(out, _decode_ref(f(q), ones, f(k), ones, f(v), 0.5), torch.bfloat16)
+    # aligned local decode: window of 100 ending at position 299
+    with torch.no_grad():
+        out = tilelang_decode(dev[0], dev[2], dev[4], scaling=0.5, short=(dev[1], dev[3]),
+                              query_position=n2 - 1, long_window=100)
+    assert_out_close(out, _decode_ref(f(q), f(k1), f(k[:, -100:]), f(v1), f(v[:, -100:]), 0.5), torch.bfloat16)
+    # bounded decode: long rows [20, 20 + 150), last 5 short rows
+    lengths = torch.tensor([150, 5, 20], dtype=torch.int32, device=cuda)
+    with torch.no_grad():
+        out = tilelang_decode(dev[0], dev[2], dev[4], scaling=0.5, short=(dev[1], dev[3]), lengths=lengths)
+    ref = _decode_ref(f(q), f(k1[:, -5:]), f(k[:, 20:170]), f(v1[:, -5:]), f(v[:, 20:170]), 0.5)
+    assert_out_close(out, ref, torch.bfloat16)
+
+
+def test_entry_point_contracts(cuda):
+    from archlab_amd import (packed_simplicial_attention, packed_simplicial_decode, simplicial_decode_attention,
+                             tilelang_attention, tilelang_decode)
+    x = [t.to(cuda) for t in _windows(1, 4, 2, 128, 17, 30, torch.float32, seed=0)]
+    with pytest.raises(ValueError, match="incompatible native decode windows"):
+        packed_simplicial_decode(*x)  # 17 short rows
+    with pytest.raises(ValueError, match="simplicial decode requires CUDA FP32 projections"):
+        simplicial_decode_attention(*(t.bfloat16() for t in x))
+    with pytest.raises(ValueError, match="incompatible one-query simplicial windows"):
+        simplicial_decode_attention(x[0], x[2], x[1], x[4], x[3])  # short axis longer than long axis
+    y = [t.to(cuda) for t in rand_inputs(1, 8, 2, 2, 64, dtype=torch.float32)]
+    with pytest.raises(ValueError, match="packed kernel requires FP32/BF16, head_dim=128, short window <=16"):
+        packed_simplicial_attention(*y, 2, 4)
+    z = [t.to(cuda) for t in rand_inputs(1, 8, 2, 2, 128, dtype=torch.bfloat16)]
+    with pytest.raises(ValueError, match="invalid attention scale/window"):
+        tilelang_attention(z[0], z[2], z[4], scaling=-1.0, long_window=4)
+    with pytest.raises(ValueError, match="TileLang attention requires CUDA BF16 inputs"):
+        tilelang_attention(z[0].float(), z[2], z[4], scaling=1.0, long_window=4)
+    with pytest.raises(ValueError, match="cached TileLang decode requires one token without gradients"):
+        tilelang_decode(z[0], z[2], z[4], scaling=1.0)

@@ -169,3 +169,27 @@ def test_paged_workload_generator_small():
     assert int(t.min()) >= 1 and len(set(t.flatten().tolist())) == t.numel()  # distinct, null page unused
     assert inp["short_cache"].shape == (2, 13, 16, 2, 64)
     assert torch.equal(inp["token_pos"], (inp["ctx"] - 1).to(torch.int32))
+
+
+def test_other_entry_point_contracts_on_cpu_tensors():
+    """Checks that fire before any device work keep the reference's messages."""
+    from archlab_amd import (deterministic_simplicial_attention, packed_simplicial_attention,
+                             packed_simplicial_decode, simplicial_decode_attention, tilelang_attention,
+                             tilelang_decode)
+    q = torch.zeros(1, 1, 4, 128)
+    k = torch.zeros(1, 8, 2, 128)
+    with pytest.raises(ValueError, match="native packed decode requires CUDA FP32"):
+        packed_simplicial_decode(q, k, k, k, k)
+    with pytest.raises(ValueError, match="simplicial decode requires CUDA FP32 projections"):
+        simplicial_decode_attention(q, k, k, k, k)
+    with pytest.raises(ValueError, match="TileLang attention requires CUDA BF16 inputs"):
+        tilelang_attention(q, k, k, scaling=1.0, long_window=4)
+    with pytest.raises(ValueError, match="TileLang attention requires CUDA BF16 inputs"):
+        tilelang_decode(q, k, k, scaling=1.0)
+    x = torch.zeros(1, 8, 2, 128)
+    with pytest.raises(ValueError, match="packed kernel requires CUDA"):
+        packed_simplicial_attention(x, x, x, x, x, 2, 4)
+    with pytest.raises(ValueError, match="require 1 <= short_window <= long_window"):
+        packed_simplicial_attention(x, x, x, x, x, 5, 4)
+    with pytest.raises(ValueError, match="deterministic simplicial core requires supported CUDA FP32 head geometry"):
+        deterministic_simplicial_attention(x, x, x, x, x, 2, 4)
