@@ -20,6 +20,12 @@
  *   sa_paged_workspace_bytes  size of the split partials that the reference
  *                             allocates with torch.empty/full/zeros
  *                             (simplicial_paged.py:112-114).
+ *   sa_prefill_bwd            replaces SimplicialFunction.backward / _backward
+ *                             (simplicial_kernels.py:133-143, :55-106) and the
+ *                             deterministic backward
+ *                             (simplicial_deterministic.py:86-104): gradients
+ *                             of q, k1, k2, v1, v2 without atomics.
+ *   sa_prefill_bwd_workspace_bytes  size of its per-(token, head) delta buffer.
  *
  * Conventions
  *   - All pointers are device pointers; strides are in ELEMENTS; the last
@@ -114,6 +120,30 @@ typedef struct sa_paged_args {
 
 /* Dense or packed-varlen prefill forward: out and (optionally) lse. */
 int sa_prefill_fwd(const sa_prefill_args* args, sa_stream_t stream);
+
+typedef struct sa_prefill_bwd_args {
+  sa_prefill_args fwd;   /* the forward call: out = its output, lse (required) its LSE */
+  const void* dout;      /* [tokens, heads_q, DV] dtype: gradient of out */
+  int64_t do_stride_t, do_stride_h;
+  void* dq;              /* [tokens, heads_q, D]   dtype */
+  int64_t dq_stride_t, dq_stride_h;
+  void* dk1;             /* [tokens, heads_kv, D]  dtype */
+  void* dk2;             /* [tokens, heads_kv, D]  dtype, strides shared with dk1 */
+  int64_t dk_stride_t, dk_stride_h;
+  void* dv1;             /* [tokens, heads_kv, DV] dtype */
+  void* dv2;             /* [tokens, heads_kv, DV] dtype, strides shared with dv1 */
+  int64_t dv_stride_t, dv_stride_h;
+  const float* dlse;     /* [tokens, heads_q] fp32 gradient of lse (dlse[t * dlse_stride_t + h]), or NULL */
+  int64_t dlse_stride_t;
+} sa_prefill_bwd_args;
+
+/* Bytes of device workspace sa_prefill_bwd needs (256-byte aligned). */
+size_t sa_prefill_bwd_workspace_bytes(const sa_prefill_bwd_args* args);
+
+/* Backward of sa_prefill_fwd: writes dq, dk1, dk2, dv1, dv2 (each exactly
+ * once, fixed reduction order: bitwise reproducible). */
+int sa_prefill_bwd(const sa_prefill_bwd_args* args, void* workspace, size_t workspace_bytes,
+                   sa_stream_t stream);
 
 /* Bytes of device workspace sa_paged_fwd needs for these arguments. */
 size_t sa_paged_workspace_bytes(const sa_paged_args* args);

@@ -61,8 +61,20 @@ class PagedArgs(ctypes.Structure):
     ]
 
 
+class PrefillBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("fwd", PrefillArgs),
+        ("dout", _vp), ("do_stride_t", _i64), ("do_stride_h", _i64),
+        ("dq", _vp), ("dq_stride_t", _i64), ("dq_stride_h", _i64),
+        ("dk1", _vp), ("dk2", _vp), ("dk_stride_t", _i64), ("dk_stride_h", _i64),
+        ("dv1", _vp), ("dv2", _vp), ("dv_stride_t", _i64), ("dv_stride_h", _i64),
+        ("dlse", _vp), ("dlse_stride_t", _i64),
+    ]
+
+
 EXPORTS = ("sa_prefill_fwd", "sa_paged_fwd", "sa_paged_workspace_bytes", "sa_paged_splits",
-           "sa_prefill_kernel", "sa_paged_kernel", "sa_last_error", "sa_version")
+           "sa_prefill_kernel", "sa_paged_kernel", "sa_last_error", "sa_version",
+           "sa_prefill_bwd", "sa_prefill_bwd_workspace_bytes")
 
 _lib = None
 _lock = threading.Lock()
@@ -97,6 +109,10 @@ def load():
         lib.sa_prefill_kernel.restype = ctypes.c_char_p
         lib.sa_paged_kernel.argtypes = [ctypes.POINTER(PagedArgs)]
         lib.sa_paged_kernel.restype = ctypes.c_char_p
+        lib.sa_prefill_bwd.argtypes = [ctypes.POINTER(PrefillBwdArgs), _vp, ctypes.c_size_t, _vp]
+        lib.sa_prefill_bwd.restype = ctypes.c_int
+        lib.sa_prefill_bwd_workspace_bytes.argtypes = [ctypes.POINTER(PrefillBwdArgs)]
+        lib.sa_prefill_bwd_workspace_bytes.restype = ctypes.c_size_t
         lib.sa_last_error.argtypes = []
         lib.sa_last_error.restype = ctypes.c_char_p
         lib.sa_version.argtypes = []

@@ -70,7 +70,11 @@ def _kernel_checks(q, v_dim, score_dim):
 
 def _forward_only(*tensors):
     if torch.is_grad_enabled() and any(t.requires_grad for t in tensors):
-        raise ValueError("simplicial attention on MI355X is forward-only: no backward kernel is provided")
+        raise ValueError("this entry point is forward-only: no backward kernel is provided for it")
+
+
+def _needs_grad(*tensors):
+    return torch.is_grad_enabled() and any(t.requires_grad for t in tensors)
 
 
 def _kernel_flag(kernel):
@@ -108,6 +112,74 @@ def _prefill(q, k1, k2, v1, v2, short_window, long_window, scale, cu_seqlens, nu
     return out, lse
 
 
+def _backward(q, k1, k2, v1, v2, out, lse, dout, dlse, short_window, long_window, scale, cu_seqlens, num_seqs,
+              seqlen):
+    """Gradients of q, k1, k2, v1, v2 ([T,H,*] contiguous) through the C ABI."""
+    lib = _native.load()
+    tokens, hq, d = q.shape
+    hk, dv = k1.shape[1], v1.shape[-1]
+    dout = dout.contiguous()
+    grads = [torch.empty_like(x) for x in (q, k1, k2, v1, v2)]
+    dq, dk1, dk2, dv1, dv2 = grads
+    fwd = _native.PrefillArgs(
+        q=q.data_ptr(), k1=k1.data_ptr(), k2=k2.data_ptr(), v1=v1.data_ptr(), v2=v2.data_ptr(),
+        out=out.data_ptr(), lse=lse.data_ptr(),
+        cu_seqlens=cu_seqlens.data_ptr() if cu_seqlens is not None else None,
+        q_stride_t=q.stride(0), q_stride_h=q.stride(1), k_stride_t=k1.stride(0), k_stride_h=k1.stride(1),
+        v_stride_t=v1.stride(0), v_stride_h=v1.stride(1), o_stride_t=out.stride(0), o_stride_h=out.stride(1),
+        lse_stride_t=hq, num_seqs=num_seqs, seqlen=seqlen, total_tokens=tokens,
+        heads_q=hq, heads_kv=hk, head_dim=d, value_dim=dv,
+        short_window=int(short_window), long_window=int(long_window), scale=scale,
+        dtype=_native.dtype_code(q.dtype), flags=0)
+    if dlse is not None:
+        dlse = dlse.float().contiguous()
+    args = _native.PrefillBwdArgs(
+        fwd=fwd, dout=dout.data_ptr(), do_stride_t=dout.stride(0), do_stride_h=dout.stride(1),
+        dq=dq.data_ptr(), dq_stride_t=dq.stride(0), dq_stride_h=dq.stride(1),
+        dk1=dk1.data_ptr(), dk2=dk2.data_ptr(), dk_stride_t=dk1.stride(0), dk_stride_h=dk1.stride(1),
+        dv1=dv1.data_ptr(), dv2=dv2.data_ptr(), dv_stride_t=dv1.stride(0), dv_stride_h=dv1.stride(1),
+        dlse=dlse.data_ptr() if dlse is not None else None, dlse_stride_t=hq)
+    nbytes = lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args))
+    workspace = torch.empty(max(nbytes, 1) + 256, device=q.device, dtype=torch.uint8)
+    aligned = (workspace.data_ptr() + 255) & ~255
+    with torch.cuda.device(q.device):
+        _native.check(lib.sa_prefill_bwd(ctypes.byref(args), aligned, nbytes, _native.stream_handle(q.device)))
+    return grads
+
+
+class _SimplicialFunction(torch.autograd.Function):
+    """Forward kernels + the atomics-free backward (sa_prefill_bwd) on [T, H, *] tensors."""
+
+    @staticmethod
+    def forward(ctx, q, k1, k2, v1, v2, short_window, long_window, scale, cu_seqlens, num_seqs, seqlen, kernel):
+        out, lse = _prefill(q, k1, k2, v1, v2, short_window, long_window, scale, cu_seqlens, num_seqs, seqlen,
+                            True, kernel)
+        ctx.save_for_backward(q, k1, k2, v1, v2, out, lse)
+        ctx.cu_seqlens = cu_seqlens
+        ctx.meta = (short_window, long_window, scale, num_seqs, seqlen)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, dout, dlse):
+        q, k1, k2, v1, v2, out, lse = ctx.saved_tensors
+        short_window, long_window, scale, num_seqs, seqlen = ctx.meta
+        if dout is None:
+            dout = torch.zeros_like(out)
+        grads = _backward(q, k1, k2, v1, v2, out, lse, dout, dlse, short_window, long_window, scale,
+                          ctx.cu_seqlens, num_seqs, seqlen)
+        return (*grads, None, None, None, None, None, None, None)
+
+
+def _prefill_autograd(q, k1, k2, v1, v2, short_window, long_window, scale, cu_seqlens, num_seqs, seqlen,
+                      return_lse, kernel):
+    if _needs_grad(q, k1, k2, v1, v2):
+        out, lse = _SimplicialFunction.apply(q, k1, k2, v1, v2, short_window, long_window, scale, cu_seqlens,
+                                             num_seqs, seqlen, kernel)
+        return out, (lse if return_lse else None)
+    return _prefill(q, k1, k2, v1, v2, short_window, long_window, scale, cu_seqlens, num_seqs, seqlen,
+                    return_lse, kernel)
+
+
 def simplicial_attention(q, k1, k2, v1, v2, short_window, long_window, *, scale=None,
                          return_lse=False, kernel="auto"):
     """Drop-in for ``simplicial_attention`` (simplicial_attention.py:77-97), forward only.
@@ -119,20 +191,20 @@ def simplicial_attention(q, k1, k2, v1, v2, short_window, long_window, *, scale=
     kernel, everything else on the portable kernel), "mfma" (raise if not
     covered) or "generic".
 
-    Deviation from the reference: the forward is deterministic (no atomics),
-    so ``torch.use_deterministic_algorithms(True)`` is allowed; inputs that
-    require grad raise ValueError because no backward kernel exists.
+    Inputs that require grad get gradients from the library's backward
+    (``sa_prefill_bwd``: atomics-free, bitwise reproducible).  Deviation from
+    the reference: forward and backward are deterministic, so
+    ``torch.use_deterministic_algorithms(True)`` is allowed.
     """
     validate_inputs(q, k1, k2, v1, v2, short_window, long_window, allow_value_dim=True)
     scale = _score_scale(scale, q.shape[-1])
     _kernel_checks(q, v1.shape[-1], q.shape[-1])
-    _forward_only(q, k1, k2, v1, v2)
     b, n, hq, d = q.shape
     hk, dv = k1.shape[2], v1.shape[-1]
     q_, k1_, k2_ = (x.contiguous().view(b * n, -1, d) for x in (q, k1, k2))
     v1_, v2_ = (x.contiguous().view(b * n, hk, dv) for x in (v1, v2))
-    out, lse = _prefill(q_, k1_, k2_, v1_, v2_, short_window, long_window, scale, None, b, n,
-                        return_lse, kernel)
+    out, lse = _prefill_autograd(q_, k1_, k2_, v1_, v2_, short_window, long_window, scale, None, b, n,
+                                 return_lse, kernel)
     out = out.view(b, n, hq, dv)
     if return_lse:
         return out, lse.view(b, n, hq)
@@ -157,14 +229,13 @@ def simplicial_varlen_attention(q, k1, k2, v1, v2, cu_seqlens, short_window, lon
                     allow_value_dim=True)
     scale = _score_scale(scale, q.shape[-1])
     _kernel_checks(q, v1.shape[-1], q.shape[-1])
-    _forward_only(q, k1, k2, v1, v2)
     if (cu_seqlens.ndim != 1 or cu_seqlens.dtype != torch.int32 or cu_seqlens.numel() < 2
             or cu_seqlens.device != q.device):
         raise ValueError("cu_seqlens must be int32 [num_seqs + 1] on the input device")
     t, hq, d = q.shape
     q_, k1_, k2_, v1_, v2_ = (x.contiguous() for x in (q, k1, k2, v1, v2))
-    out, lse = _prefill(q_, k1_, k2_, v1_, v2_, short_window, long_window, scale,
-                        cu_seqlens.contiguous(), cu_seqlens.numel() - 1, 0, return_lse, kernel)
+    out, lse = _prefill_autograd(q_, k1_, k2_, v1_, v2_, short_window, long_window, scale,
+                                 cu_seqlens.contiguous(), cu_seqlens.numel() - 1, 0, return_lse, kernel)
     return (out, lse) if return_lse else out
 
 

@@ -16,15 +16,16 @@ from __future__ import annotations
 
 import torch
 
-from .simplicial_attention import _forward_only, _prefill, validate_inputs
+from .simplicial_attention import _prefill_autograd, validate_inputs
 from .window_decode import window_decode
 
 
 def packed_simplicial_attention(q, k1, k2, v1, v2, w1, w2):
     """q [B,N,HQ,128] (fp32, or bf16); k1/k2/v1/v2 [B,N,HK,128] -> fp32 [B,N,HQ,128].
 
-    Deviation: forward only (inputs that require grad raise ValueError) and,
-    being deterministic, allowed under ``torch.use_deterministic_algorithms``.
+    Gradients flow through the library's backward (fp32, as the reference's
+    fp32 buffers); being deterministic, the call is allowed under
+    ``torch.use_deterministic_algorithms`` (a deviation: the reference raises).
     """
     validate_inputs(q, k1, k2, v1, v2, w1, w2, allow_scaled_query=True)
     if not q.is_cuda:
@@ -32,12 +33,11 @@ def packed_simplicial_attention(q, k1, k2, v1, v2, w1, w2):
     b, n, hq, d = q.shape
     if q.dtype not in (torch.float32, torch.bfloat16) or w1 > 16 or d != 128:
         raise ValueError("packed kernel requires FP32/BF16, head_dim=128, short window <=16")
-    _forward_only(q, k1, k2, v1, v2)
     hk = k1.shape[2]
     xs = [x.float().contiguous() for x in (q, k1, k2, v1, v2)]
     q_ = xs[0].view(b * n, hq, d)
     k1_, k2_, v1_, v2_ = (x.view(b * n, hk, d) for x in xs[1:])
-    out, _ = _prefill(q_, k1_, k2_, v1_, v2_, w1, w2, d ** -0.5, None, b, n, False, "auto")
+    out, _ = _prefill_autograd(q_, k1_, k2_, v1_, v2_, w1, w2, d ** -0.5, None, b, n, False, "auto")
     return out.view(b, n, hq, d)
 
 

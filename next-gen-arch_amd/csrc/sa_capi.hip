@@ -110,6 +110,27 @@ int sa_prefill_fwd(const sa_prefill_args* a, sa_stream_t stream) {
   return SA_OK;
 }
 
+size_t sa_prefill_bwd_workspace_bytes(const sa_prefill_bwd_args* a) {
+  if (!a || sa::check_prefill(&a->fwd) != SA_OK) return 0;
+  return sa::prefill_bwd_workspace_bytes(a);
+}
+
+int sa_prefill_bwd(const sa_prefill_bwd_args* a, void* workspace, size_t workspace_bytes, sa_stream_t stream) {
+  if (!a) return sa::fail(SA_ERR_INVALID, "null arguments");
+  int rc = sa::check_prefill(&a->fwd);
+  if (rc != SA_OK) return rc;
+  if (a->fwd.total_tokens == 0) return SA_OK;
+  if (!a->fwd.lse || !a->dout || !a->dq || !a->dk1 || !a->dk2 || !a->dv1 || !a->dv2)
+    return sa::fail(SA_ERR_INVALID, "null tensor pointer");
+  const size_t need = sa::prefill_bwd_workspace_bytes(a);
+  if (workspace_bytes < need || !workspace) return sa::fail(SA_ERR_INVALID, "workspace too small");
+  if ((uintptr_t)workspace & 255) return sa::fail(SA_ERR_INVALID, "workspace must be 256-byte aligned");
+  hipError_t e = sa::launch_prefill_bwd(a, workspace, (hipStream_t)stream);
+  if (e != hipSuccess) return sa::fail(SA_ERR_HIP, hipGetErrorString(e));
+  sa::g_last_error.clear();
+  return SA_OK;
+}
+
 const char* sa_prefill_kernel(const sa_prefill_args* a) {
   if (sa::check_prefill(a) != SA_OK) return nullptr;
   return sa::mfma_prefill_ok(a) ? "mfma" : "generic";

@@ -31,6 +31,10 @@ int paged_choose_splits(const sa_paged_args* a);
 size_t paged_workspace_bytes(const sa_paged_args* a, int splits);
 hipError_t launch_paged(const sa_paged_args* a, int splits, void* ws, size_t ws_bytes, hipStream_t stream);
 
+// Backward (sa_backward.hip).
+size_t prefill_bwd_workspace_bytes(const sa_prefill_bwd_args* a);
+hipError_t launch_prefill_bwd(const sa_prefill_bwd_args* a, void* ws, hipStream_t stream);
+
 int device_cu_count();
 
 }  // namespace sa

@@ -1,0 +1,114 @@
+"""GPU parity of the backward (sa_prefill_bwd through torch.autograd) against
+float64 autograd of the CPU oracle on the same values.
+
+Tolerances (max-abs error over a gradient tensor, relative to that tensor's
+largest reference magnitude g_max):
+  * fp32 inputs: <= 1e-4 * max(g_max, 1);
+  * bf16 inputs: <= 2e-2 * max(g_max, 1) -- the reference's backward rounds
+    a = q ⊙ k1, dout ⊙ v1, dS and P (on the value paths) to bf16
+    (simplicial_kernels.py:75-101), each a 2^-9 relative step, and the
+    gradient is returned in bf16.
+Also: the result is bitwise reproducible, the LSE output is differentiable,
+and varlen gradients equal per-sequence ones.
+"""
+
+import pytest
+import torch
+
+from helpers import rand_inputs
+from oracle import simplicial_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _ref_grads(x, ws, wl, scale, dout, dlse=None):
+    xs = [t.double().requires_grad_(True) for t in x]
+    o, l = O.reference_simplicial(*xs, ws, wl, scale=scale, return_lse=True)
+    loss = (o * dout.double()).sum()
+    if dlse is not None:
+        loss = loss + (l * dlse.double()).sum()
+    loss.backward()
+    return [t.grad.float() for t in xs]
+
+
+def _assert_grads(got, ref, dtype, label):
+    rtol = 1e-4 if dtype == torch.float32 else 2e-2
+    names = ["dq", "dk1", "dk2", "dv1", "dv2"]
+    msgs = []
+    for n, g, r in zip(names, got, ref):
+        g = g.float().cpu()
+        assert torch.isfinite(g).all(), f"{label} {n}: non-finite"
+        err = (g - r).abs().max().item()
+        bound = rtol * max(r.abs().max().item(), 1.0)
+        msgs.append(f"{n} {err:.2e}/{bound:.1e}")
+        assert err <= bound, f"{label} {n}: max-abs {err:.3e} > {bound:.3e}"
+    print(label + ": " + " ".join(msgs), flush=True)
+
+
+def _run(cuda, b, n, hq, hk, d, ws, wl, dtype, dv=None, scale=None, seed=0, dlse=False):
+    from archlab_amd import simplicial_attention
+    x = rand_inputs(b, n, hq, hk, d, dv=dv, seed=seed, dtype=dtype)
+    g = torch.Generator().manual_seed(seed + 100)
+    dout = torch.randn(b, n, hq, x[3].shape[-1], generator=g).to(dtype)
+    dl = torch.randn(b, n, hq, generator=g) if dlse else None
+    xd = [t.to(cuda).requires_grad_(True) for t in x]
+    out, lse = simplicial_attention(*xd, ws, wl, scale=scale, return_lse=True)
+    loss = (out.float() * dout.to(cuda).float()).sum()
+    if dlse:
+        loss = loss + (lse * dl.to(cuda)).sum()
+    loss.backward()
+    got = [t.grad for t in xd]
+    sc = d ** -0.5 if scale is None else scale
+    ref = _ref_grads([t.float() for t in x], ws, wl, sc, dout.float(), dl)
+    _assert_grads(got, ref, dtype, f"b{b} n{n} h{hq}/{hk} d{d} dv{dv or d} w{ws}x{wl} {dtype}")
+    return xd, got
+
+
+@pytest.mark.parametrize("hq,hk,d,ws,wl", [(4, 2, 32, 5, 12), (2, 2, 64, 1, 1), (6, 3, 16, 3, 40),
+                                           (4, 4, 128, 8, 8)])
+def test_backward_fp32(cuda, hq, hk, d, ws, wl):
+    _run(cuda, 2, 37, hq, hk, d, ws, wl, torch.float32)
+
+
+@pytest.mark.parametrize("hq,hk,d,ws,wl", [(4, 1, 64, 6, 20), (8, 2, 128, 32, 96)])
+def test_backward_bf16(cuda, hq, hk, d, ws, wl):
+    _run(cuda, 1, 70, hq, hk, d, ws, wl, torch.bfloat16)
+
+
+def test_backward_value_dim_and_scale(cuda):
+    _run(cuda, 1, 29, 4, 2, 32, 4, 9, torch.float32, dv=64, scale=0.3)
+
+
+def test_backward_lse_gradient(cuda):
+    _run(cuda, 1, 25, 2, 1, 32, 3, 7, torch.float32, dlse=True)
+
+
+def test_backward_deterministic(cuda):
+    from archlab_amd import simplicial_attention
+    x = [t.to(cuda) for t in rand_inputs(1, 90, 8, 2, 128, seed=4, dtype=torch.bfloat16)]
+    dout = torch.randn(1, 90, 8, 128, device=cuda).bfloat16()
+    runs = []
+    for _ in range(2):
+        xd = [t.clone().requires_grad_(True) for t in x]
+        simplicial_attention(*xd, 16, 64).backward(dout)
+        runs.append([t.grad.clone() for t in xd])
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+
+
+def test_backward_varlen_equals_per_sequence(cuda):
+    from archlab_amd import simplicial_attention, simplicial_varlen_attention
+    lengths = [9, 1, 30, 17]
+    t = sum(lengths)
+    x = [v[0] for v in rand_inputs(1, t, 4, 2, 32, seed=8, dtype=torch.float32)]
+    dout = torch.randn(t, 4, 32)
+    cu = torch.tensor([0, 9, 10, 40, 57], dtype=torch.int32, device=cuda)
+    xd = [v.to(cuda).requires_grad_(True) for v in x]
+    simplicial_varlen_attention(*xd, cu, 4, 11).backward(dout.to(cuda))
+    start = 0
+    for n in lengths:
+        xs = [v[start:start + n][None].to(cuda).requires_grad_(True) for v in x]
+        simplicial_attention(*xs, 4, 11).backward(dout[start:start + n][None].to(cuda))
+        for a, b in zip(xd, xs):
+            torch.testing.assert_close(a.grad[start:start + n], b.grad[0], rtol=0, atol=0)
+        start += n

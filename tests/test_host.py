@@ -56,7 +56,8 @@ int main(void) {{
     return {k: int(v) for k, v in (line.split() for line in res.splitlines())}
 
 
-@pytest.mark.parametrize("cls,struct", [("PrefillArgs", "sa_prefill_args"), ("PagedArgs", "sa_paged_args")])
+@pytest.mark.parametrize("cls,struct", [("PrefillArgs", "sa_prefill_args"), ("PagedArgs", "sa_paged_args"),
+                                        ("PrefillBwdArgs", "sa_prefill_bwd_args")])
 def test_python_binding_matches_c_struct_layout(cls, struct):
     from archlab_amd import _native
     py = getattr(_native, cls)
