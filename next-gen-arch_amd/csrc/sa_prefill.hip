@@ -79,12 +79,15 @@ __device__ __forceinline__ int xcd_remap(int b, int n) {
 #ifndef SA_PREFILL_DEPTH
 #define SA_PREFILL_DEPTH 2
 #endif
+#ifndef SA_PREFILL_WAVES
+#define SA_PREFILL_WAVES 4
+#endif
 
 template <int D, int NQ, int NH, int P>
-__global__ __launch_bounds__(256, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_SIMD)) void prefill_mfma_kernel(PrefillParams p) {
-  static_assert(NQ * NH == 4, "4 waves per block");
+__global__ __launch_bounds__(64 * NQ * NH, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_SIMD)) void prefill_mfma_kernel(PrefillParams p) {
+  static_assert(NQ * NH == 4 || NQ * NH == 8, "4 or 8 waves per block");
   static_assert(P >= 1 && P <= 4, "prefetch depth");
-  constexpr int NW = 4;
+  constexpr int NW = NQ * NH;
   constexpr int ROWS = kChunk + NQ - 1;  // tile rows: one chunk of all NQ queries
   using G = TileGeom<D, ROWS, NW>;
   constexpr int R = P + 1;  // ring slots for the long-axis tiles
@@ -93,7 +96,7 @@ __global__ __launch_bounds__(256, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_SIMD)) vo
   constexpr bool kPipelined = D <= 128 && P >= 2;
   extern __shared__ __attribute__((aligned(16))) char lds[];
   // One more slot after the ring holds the short window of the pass: its K
-  // region takes the k1 rows and (in its V region) the q rows of the 4 waves
+  // region takes the k1 rows and (in its V region) the q rows of the NW waves
   // at the start of the pass; the v1 rows replace the q rows during the last
   // chunk.  All of it arrives by DMA, 1 KB per instruction.
   char* const sslot = lds + R * G::SLOT;
@@ -175,15 +178,15 @@ __global__ __launch_bounds__(256, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_SIMD)) vo
   auto issue = [&](int c) {
     dma_tile(std::integral_constant<int, 0>{}, lds + (c % R) * G::SLOT, kb0 + kChunk * c, p.k2, p.v2);
   };
-  // q rows of the 4 waves into rows 0..3 of the short slot's V region (wave 0)
+  // q rows of the NW waves into rows 0..NW-1 of the short slot's V region (wave 0)
   auto dma_q = [&]() {
     if (wid == 0) {
-      constexpr int QI = (4 * G::RS + 1023) / 1024;
+      constexpr int QI = (NW * G::RS + 1023) / 1024;
 #pragma unroll
       for (int k = 0; k < QI; ++k) {
         const int b = k * 1024 + lane * 16;
         int row = b / G::RS, seg = (b % G::RS) >> 4;
-        if (row >= 4 || seg >= G::kSegs) row = 0, seg = 0;
+        if (row >= NW || seg >= G::kSegs) row = 0, seg = 0;
         const int tq = min(t0 + row / NH, last);
         const int hq = g * p.group + hs * NH + row % NH;
         dma16(p.q + (int64_t)tq * p.q_st + (int64_t)hq * p.q_sh + seg * 8, sslot + G::VOFF + k * 1024);
@@ -347,14 +350,15 @@ static hipError_t launch_prefill_mfma(const PrefillParams& base_p, hipStream_t s
   p.qblocks = (p.total + NQ - 1) / NQ;
   p.hsub = p.group / NH;
   p.nblocks = p.qblocks * p.hk * p.hsub;
-  using G = TileGeom<D, kChunk + NQ - 1, 4>;
+  constexpr int NW = NQ * NH;
+  using G = TileGeom<D, kChunk + NQ - 1, NW>;
   size_t lds = (size_t)(P + 2) * G::SLOT;  // P + 1 ring slots + the short-window slot
-  const size_t red = (size_t)4 * 64 * 36 * sizeof(float);
+  const size_t red = (size_t)NW * 64 * 36 * sizeof(float);
   if (lds < red) lds = red;
   auto kern = prefill_mfma_kernel<D, NQ, NH, P>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3(p.nblocks), dim3(256), lds, stream, p);
+  hipLaunchKernelGGL(kern, dim3(p.nblocks), dim3(64 * NW), lds, stream, p);
   return hipGetLastError();
 }
 
@@ -367,6 +371,11 @@ static hipError_t dispatch_prefill_mfma_d(const PrefillParams& p, hipStream_t st
     if (G % 4 == 0) return launch_prefill_mfma<D, 1, 4, 2>(p, stream);
     if (G % 2 == 0) return launch_prefill_mfma<D, 2, 2, 2>(p, stream);
     return launch_prefill_mfma<D, 4, 1, 2>(p, stream);
+  } else if constexpr (SA_PREFILL_WAVES == 8) {
+    // one 8-wave workgroup per CU: a tile serves twice the queries
+    if (G % 4 == 0) return launch_prefill_mfma<D, 2, 4, 3>(p, stream);
+    if (G % 2 == 0) return launch_prefill_mfma<D, 4, 2, 3>(p, stream);
+    return launch_prefill_mfma<D, 8, 1, 3>(p, stream);
   } else {
     constexpr int P = SA_PREFILL_DEPTH;
     if (G % 4 == 0) return launch_prefill_mfma<D, 1, 4, P>(p, stream);
