@@ -2,8 +2,8 @@
 
 Forward-path drop-in for archlab's ``simplicial_attention`` and
 ``simplicial_paged_attention`` (and the entry points that compute the same
-attention: the contiguous / packed decodes, the deterministic form and the
-TileLang signatures); the kernels are hand-written gfx950 HIP behind the C ABI
+attention: the contiguous / packed decodes, the deterministic form, the determinant
+scores and the TileLang signatures); the kernels are hand-written gfx950 HIP behind the C ABI
 of ``include/simplicial_mi355x.h``.
 """
 
@@ -13,6 +13,11 @@ from .architectures.simplicial_attention import (  # noqa: F401
     validate_inputs,
 )
 from .architectures.simplicial_decode import simplicial_decode_attention  # noqa: F401
+from .architectures.simplicial_determinant import (  # noqa: F401
+    determinant_operands,
+    determinant_simplicial_attention,
+    oriented_determinant_simplicial_attention,
+)
 from .architectures.simplicial_deterministic import deterministic_simplicial_attention  # noqa: F401
 from .architectures.simplicial_packed import (  # noqa: F401
     packed_simplicial_attention,
@@ -34,4 +39,7 @@ __all__ = [
     "packed_simplicial_decode",
     "tilelang_attention",
     "tilelang_decode",
+    "determinant_operands",
+    "determinant_simplicial_attention",
+    "oriented_determinant_simplicial_attention",
 ]

@@ -24,6 +24,13 @@ It restates, in plain PyTorch on the CPU, what the reference computes:
 * ``token_layout`` follows ``src/archlab/training/serving.py:52-62``.
 * ``causal_pairs`` / ``causal_triples`` follow
   ``src/archlab/architectures/limite_cost.py:31-45``.
+* ``determinant_reference`` / ``reference_determinant_simplicial`` follow
+  ``src/archlab/architectures/simplicial_attention.py:151-178`` (and the
+  any-window form of ``tests/test_simplicial_determinant.py:173-189``): the
+  score of (q, k1_j, k2_k) is the sum over 3-coordinate chunks of the signed
+  3x3 determinant det([q; k1_j; k2_k]) (trailing dim % 3 coordinates take no
+  part), evaluated with ``torch.linalg.det`` and independent of any operand
+  expansion.
 
 Argument names follow the reference: ``(k1, v1, short_window)`` is one key
 axis and ``(k2, v2, long_window)`` the other.  Every check of this file lives
@@ -227,3 +234,51 @@ def causal_triples(length, short_span, long_span):
     return (a * (a + 1) * (2 * a + 1) // 6
             + a * (b * (b + 1) - a * (a + 1)) // 2
             + (length - b) * a * b)
+
+
+def determinant_reference(q, k1, k2, v1, v2, window_1, window_2, *, query_positions=None, scale=None):
+    """Determinant-score attention with any positive windows (k1 within window_1, k2 within window_2).
+
+    Follows simplicial_attention.py:151-178 (and the any-window oracle of
+    tests/test_simplicial_determinant.py:173-189): per query i and chunk c of
+    3 coordinates, score_c = det([q_i[c]; k1_j[c]; k2_k[c]]); the joint softmax
+    runs over all (j, k) with i-window_1 < j <= i and i-window_2 < k <= i;
+    O_i = sum P_ijk (v1_j * v2_k).  Default scale 1/sqrt(score_dim) of the
+    unexpanded width.  Use float32/float64 (torch.linalg.det has no bf16).
+    """
+    if q.shape[-1] < 3:
+        raise ValueError("determinant scores require at least 3 coordinates")
+    if q.dtype not in (torch.float32, torch.float64):
+        raise ValueError("determinant oracle requires float32/float64")
+    if min(window_1, window_2) < 1:
+        raise ValueError("windows must be positive")
+    scale = _score_scale(scale, q.shape[-1])
+    groups = q.shape[2] // k1.shape[2]
+    k1, k2, v1, v2 = [x.repeat_interleave(groups, dim=2) for x in (k1, k2, v1, v2)]
+    chunks = q.shape[-1] // 3
+    qc, k1c, k2c = (x[..., :3 * chunks].reshape(*x.shape[:-1], chunks, 3) for x in (q, k1, k2))
+    positions = range(q.shape[1]) if query_positions is None else query_positions
+    outs = []
+    for i in positions:
+        if not 0 <= i < q.shape[1]:
+            raise ValueError("oracle query position outside sequence")
+        j0, k0 = max(0, i - window_1 + 1), max(0, i - window_2 + 1)
+        a = qc[:, i]                      # [B,H,C,3]
+        b = k1c[:, j0:i + 1]              # [B,J,H,C,3]
+        c = k2c[:, k0:i + 1]              # [B,K,H,C,3]
+        nj, nk = b.shape[1], c.shape[1]
+        rows = torch.stack(torch.broadcast_tensors(a[:, None, None], b[:, :, None], c[:, None]), dim=-2)
+        scores = torch.linalg.det(rows).sum(-1)            # [B,J,K,H]
+        p = (scores * scale).permute(0, 3, 1, 2).reshape(q.shape[0], q.shape[2], nj * nk).softmax(-1)
+        p = p.reshape(q.shape[0], q.shape[2], nj, nk)
+        outs.append(torch.einsum("bhjk,bjhd,bkhd->bhd", p, v1[:, j0:i + 1], v2[:, k0:i + 1]))
+    return torch.stack(outs, dim=1)
+
+
+def reference_determinant_simplicial(q, k1, k2, v1, v2, short_window, long_window, *,
+                                     query_positions=None, scale=None):
+    """simplicial_attention.py:151-178: the determinant oracle with 1 <= short <= long."""
+    if min(short_window, long_window) < 1 or short_window > long_window:
+        raise ValueError("require 1 <= short_window <= long_window")
+    return determinant_reference(q, k1, k2, v1, v2, short_window, long_window,
+                                 query_positions=query_positions, scale=scale)

@@ -1,0 +1,92 @@
+"""GPU parity of the determinant-score entry points (simplicial_attention.py:100-202).
+
+``determinant_simplicial_attention`` and
+``oriented_determinant_simplicial_attention`` run the library's prefill
+forward and backward on the Sarrus-expanded operands (score width DS = the
+padded expansion, value width DV unchanged).  The checker is the CPU
+determinant oracle (``torch.linalg.det`` per 3-coordinate chunk, fp64,
+autograd for the gradients), which shares no code with the expansion.
+
+Tolerances follow the reference's GPU test
+(tests/test_simplicial_determinant.py:121-170): relative L2 error of the
+output and of each of the five gradients below 1e-4 (fp32) or 2.5e-2
+(bf16); the bf16 output additionally meets the max-abs gate of 2e-2.
+"""
+
+import pytest
+import torch
+
+from helpers import assert_out_close
+from oracle import simplicial_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(score_dim, value_dim, n, heads=16, kv_heads=4, seed=731):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(1, n, h, d, generator=g, dtype=torch.float64) * 0.5
+            for h, d in ((heads, score_dim), (kv_heads, score_dim), (kv_heads, score_dim),
+                         (kv_heads, value_dim), (kv_heads, value_dim))]
+
+
+def _check(actual, grads, expected, exp_grads, dtype):
+    tol = 2.5e-2 if dtype == torch.bfloat16 else 1e-4
+    errs = {}
+    for name, a, e in zip(("out", "dq", "dk1", "dk2", "dv1", "dv2"), (actual, *grads), (expected, *exp_grads)):
+        a = a.detach().cpu().double()
+        e = e.detach()
+        assert torch.isfinite(a).all(), name
+        rel = float((a - e).norm() / e.norm().clamp_min(1e-12))
+        errs[name] = rel
+        assert rel < tol or float((a - e).abs().max()) < tol * 0.01, (name, rel)
+    if dtype == torch.bfloat16:
+        assert_out_close(actual, expected, dtype)
+    return errs
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("ds,dv,n,short,long,scale", [
+    (8, 16, 37, 2, 35, 0.2),      # minimum padded width (16) and a partial chunk
+    (64, 64, 40, 3, 21, None),    # DS 128 / DV 64
+    (128, 128, 45, 5, 33, None),  # DS 256 / DV 128
+    (256, 256, 6, 6, 6, None),    # DS 512 / DV 256
+    (256, 256, 17, 2, 17, None),
+])
+def test_determinant_forward_backward(cuda, dtype, ds, dv, n, short, long, scale):
+    from archlab_amd import determinant_simplicial_attention
+    x64 = _inputs(ds, dv, n)
+    inputs = [t.to(cuda, dtype).requires_grad_() for t in x64]
+    refs = [t.to(dtype).double().requires_grad_() for t in x64]  # the values the kernel sees
+    kw = {} if scale is None else {"scale": scale}
+    actual = determinant_simplicial_attention(*inputs, short, long, **kw)
+    expected = O.reference_determinant_simplicial(*refs, short, long, **kw)
+    dy = torch.randn(expected.shape, generator=torch.Generator().manual_seed(753), dtype=torch.float64).to(dtype)
+    grads = torch.autograd.grad(actual, inputs, dy.to(cuda))
+    exp_grads = torch.autograd.grad(expected, refs, dy.double())
+    errs = _check(actual, grads, expected, exp_grads, dtype)
+    print(f"det ds={ds} dv={dv} n={n} w=({short},{long}) {dtype}: " +
+          " ".join(f"{k}={v:.1e}" for k, v in errs.items()))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("d,w1,w2", [(256, 19, 3), (256, 3, 19), (128, 17, 5)])
+def test_oriented_determinant_windows(cuda, dtype, d, w1, w2):
+    from archlab_amd import oriented_determinant_simplicial_attention
+    x64 = _inputs(d, d, 21)
+    inputs = [t.to(cuda, dtype).requires_grad_() for t in x64]
+    refs = [t.to(dtype).double().requires_grad_() for t in x64]
+    actual = oriented_determinant_simplicial_attention(*inputs, w1, w2)
+    expected = O.determinant_reference(*refs, w1, w2)
+    dy = torch.randn(expected.shape, generator=torch.Generator().manual_seed(911), dtype=torch.float64).to(dtype)
+    grads = torch.autograd.grad(actual, inputs, dy.to(cuda))
+    exp_grads = torch.autograd.grad(expected, refs, dy.double())
+    _check(actual, grads, expected, exp_grads, dtype)
+
+
+def test_determinant_single_pair_has_no_score_gradient(cuda):
+    from archlab_amd import determinant_simplicial_attention
+    inputs = [t.to(cuda, torch.float32).requires_grad_() for t in _inputs(8, 16, 5)]
+    out = determinant_simplicial_attention(*inputs, 1, 1)
+    torch.testing.assert_close(out.cpu(), (inputs[3] * inputs[4]).detach().cpu().repeat_interleave(4, dim=2))
+    grads = torch.autograd.grad(out.sum(), inputs)
+    assert all(not g.count_nonzero() for g in grads[:3])

@@ -194,3 +194,50 @@ def test_other_entry_point_contracts_on_cpu_tensors():
         packed_simplicial_attention(x, x, x, x, x, 5, 4)
     with pytest.raises(ValueError, match="deterministic simplicial core requires supported CUDA FP32 head geometry"):
         deterministic_simplicial_attention(x, x, x, x, x, 2, 4)
+
+
+@pytest.mark.parametrize("d,width", [(3, 16), (8, 16), (64, 128), (128, 256), (256, 512)])
+def test_determinant_operands_expand_to_the_determinant_sum(d, width):
+    """The product's Sarrus expansion (pure tensor indexing) against the oracle's linalg.det."""
+    from archlab_amd import determinant_operands
+    g = torch.Generator().manual_seed(d)
+    q, k1, k2 = (torch.randn(3, 5, d, generator=g, dtype=torch.float64) for _ in range(3))
+    a, b, c = determinant_operands(q, k1, k2)
+    assert a.shape[-1] == b.shape[-1] == c.shape[-1] == width
+    used = d - d % 3
+    chunks = [x[..., :used].reshape(3, 5, used // 3, 3) for x in (q, k1, k2)]
+    expected = torch.linalg.det(torch.stack(chunks, dim=-2)).sum(-1)
+    torch.testing.assert_close((a * b * c).sum(-1), expected, atol=1e-10, rtol=1e-10)
+    assert not a[..., 2 * used:].count_nonzero() and not b[..., 2 * used:].count_nonzero()
+
+
+def test_determinant_expansion_through_the_trilinear_oracle():
+    """Expanded operands + the trilinear oracle == the determinant oracle (two independent paths)."""
+    from archlab_amd import determinant_operands
+    from oracle import simplicial_oracle as O
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(1, 6, 4, 8, generator=g, dtype=torch.float64)
+    k1, k2 = (torch.randn(1, 6, 2, 8, generator=g, dtype=torch.float64) for _ in range(2))
+    v1, v2 = (torch.randn(1, 6, 2, 5, generator=g, dtype=torch.float64) for _ in range(2))
+    qs, k1s, k2s = determinant_operands(q, k1, k2)
+    got = O.reference_simplicial(qs, k1s, k2s, v1, v2, 2, 4, scale=8 ** -0.5)
+    torch.testing.assert_close(got, O.reference_determinant_simplicial(q, k1, k2, v1, v2, 2, 4),
+                               atol=1e-12, rtol=1e-10)
+
+
+def test_determinant_entry_point_contracts_on_cpu_tensors():
+    from archlab_amd import (determinant_operands, determinant_simplicial_attention,
+                             oriented_determinant_simplicial_attention)
+    x = torch.zeros(1, 4, 2, 8)
+    with pytest.raises(ValueError, match="at least 3 coordinates"):
+        determinant_operands(x[..., :2], x[..., :2], x[..., :2])
+    with pytest.raises(ValueError, match="matching score widths"):
+        determinant_operands(x, x[..., :6], x)
+    with pytest.raises(ValueError, match="positive integers"):
+        oriented_determinant_simplicial_attention(x, x, x, x, x, 0, 2)
+    with pytest.raises(ValueError, match="backend must be kernel or reference"):
+        oriented_determinant_simplicial_attention(x, x, x, x, x, 1, 2, backend="triton")
+    with pytest.raises(ValueError, match="not shipped"):
+        oriented_determinant_simplicial_attention(x, x, x, x, x, 1, 2, backend="reference")
+    with pytest.raises(ValueError, match="kernel supports CUDA"):
+        determinant_simplicial_attention(x, x, x, x, x, 1, 2)

@@ -261,3 +261,95 @@ def test_kernel_rounding_reference_pinned():
     torch.testing.assert_close(l3, l, rtol=1e-12, atol=1e-12)
     o4, l4 = O.kernel_rounding_reference(*x, 3, 6)
     assert 0 < (l4 - l2).abs().max() < 0.05
+
+
+# ---- determinant scores (oracle.determinant_reference) ----------------------
+
+def _det_inputs(d, dv, n=5, hq=4, hk=2, seed=731):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(1, n, h, w, generator=g, dtype=torch.float64) * 0.5
+            for h, w in ((hq, d), (hk, d), (hk, d), (hk, dv), (hk, dv))]
+
+
+def _leibniz_det3(a, b, c):
+    """3x3 determinant of rows a, b, c by the permutation (Leibniz) sum."""
+    rows = (a, b, c)
+    total = 0.0
+    for perm, sign in (((0, 1, 2), 1), ((1, 2, 0), 1), ((2, 0, 1), 1),
+                       ((0, 2, 1), -1), ((2, 1, 0), -1), ((1, 0, 2), -1)):
+        total += sign * rows[0][perm[0]] * rows[1][perm[1]] * rows[2][perm[2]]
+    return total
+
+
+def _brute_determinant(q, k1, k2, v1, v2, w1, w2, scale):
+    """Scalar loops: Leibniz determinants, explicit softmax, explicit output."""
+    b, n, hq, d = q.shape
+    hk, dv = k1.shape[2], v1.shape[-1]
+    out = torch.zeros(b, n, hq, dv, dtype=torch.float64)
+    for bi in range(b):
+        for i in range(n):
+            for h in range(hq):
+                g = h // (hq // hk)
+                pairs = []
+                for j in range(max(0, i - w1 + 1), i + 1):
+                    for k in range(max(0, i - w2 + 1), i + 1):
+                        s = 0.0
+                        for c in range(d // 3):
+                            sl = slice(3 * c, 3 * c + 3)
+                            s += _leibniz_det3(q[bi, i, h, sl].tolist(), k1[bi, j, g, sl].tolist(),
+                                               k2[bi, k, g, sl].tolist())
+                        pairs.append((scale * s, j, k))
+                m = max(p[0] for p in pairs)
+                z = sum(math.exp(p[0] - m) for p in pairs)
+                for s, j, k in pairs:
+                    out[bi, i, h] += math.exp(s - m) / z * v1[bi, j, g] * v2[bi, k, g]
+    return out
+
+
+@pytest.mark.parametrize("d,dv,w1,w2", [(3, 2, 2, 3), (8, 5, 2, 3), (7, 4, 4, 1)])
+def test_determinant_oracle_matches_leibniz_brute_force(d, dv, w1, w2):
+    x = _det_inputs(d, dv)
+    got = O.determinant_reference(*x, w1, w2, scale=0.7)
+    torch.testing.assert_close(got, _brute_determinant(*x, w1, w2, 0.7), atol=1e-12, rtol=1e-10)
+
+
+def test_determinant_oracle_chunk_rotations_and_reflections():
+    """A common proper rotation per 3-chunk keeps every determinant; a reflection negates them."""
+    x = _det_inputs(6, 4, n=6)
+    g = torch.Generator().manual_seed(5)
+    rot, _ = torch.linalg.qr(torch.randn(2, 3, 3, generator=g, dtype=torch.float64))
+    rot[..., -1] *= torch.linalg.det(rot)[..., None]  # det +1
+
+    def apply(t, m):
+        return torch.einsum("...ci,cij->...cj", t.reshape(*t.shape[:-1], 2, 3), m).reshape(t.shape)
+
+    ref = O.determinant_reference(*x, 2, 4, scale=0.9)
+    rotated = [apply(t, rot) for t in x[:3]] + x[3:]
+    torch.testing.assert_close(O.determinant_reference(*rotated, 2, 4, scale=0.9), ref)
+    rot[..., 0] *= -1  # det -1: every chunk determinant flips sign, i.e. the scale does
+    reflected = [apply(t, rot) for t in x[:3]] + x[3:]
+    torch.testing.assert_close(O.determinant_reference(*reflected, 2, 4, scale=0.9),
+                               O.determinant_reference(*x, 2, 4, scale=-0.9))
+
+
+def test_determinant_oracle_axis_exchange_and_trailing_coordinates():
+    x = _det_inputs(8, 5, n=7)
+    q, k1, k2, v1, v2 = x
+    # det([-q; k2; k1]) == det([q; k1; k2]) and v2*v1 == v1*v2: the axes exchange
+    torch.testing.assert_close(O.determinant_reference(q, k1, k2, v1, v2, 5, 2),
+                               O.determinant_reference(-q, k2, k1, v2, v1, 2, 5))
+    # the trailing dim % 3 = 2 coordinates take no part in the score
+    alt = [t.clone() for t in (q, k1, k2)]
+    for t in alt:
+        t[..., 6:] += 3.0
+    torch.testing.assert_close(O.determinant_reference(*alt, v1, v2, 2, 3), O.determinant_reference(*x, 2, 3))
+    # one pair per query: the output is v1 * v2 of the query's own position
+    torch.testing.assert_close(O.determinant_reference(*x, 1, 1),
+                               (v1 * v2).repeat_interleave(2, dim=2))
+
+
+def test_determinant_oracle_planted_transpose_fails():
+    """Swapping k1 and k2 without negating q (a plausible slip) is caught by the brute force."""
+    q, k1, k2, v1, v2 = _det_inputs(6, 3)
+    wrong = O.determinant_reference(q, k2, k1, v1, v2, 3, 3, scale=1.0)
+    assert not torch.allclose(wrong, _brute_determinant(q, k1, k2, v1, v2, 3, 3, 1.0), atol=1e-6)
