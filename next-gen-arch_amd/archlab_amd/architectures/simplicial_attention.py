@@ -187,9 +187,10 @@ def simplicial_attention(q, k1, k2, v1, v2, short_window, long_window, *, scale=
     q [B,N,HQ,D]; k1, k2 [B,N,HK,D]; v1, v2 [B,N,HK,DV].  Returns O
     [B,N,HQ,DV] in q's dtype and, with ``return_lse=True``, also the
     natural-log LSE [B,N,HQ] in float32.  ``kernel`` selects the
-    implementation: "auto" (bf16 with D == DV in {64,128,256} runs on the MFMA
-    kernel, everything else on the portable kernel), "mfma" (raise if not
-    covered) or "generic".
+    implementation: "auto" (bf16 with D == DV in {64,128,256}, or with
+    (D, DV) = (128, 64) / (256, 128) as the determinant expansion produces,
+    runs on the MFMA kernel, everything else on the portable kernel), "mfma"
+    (raise if not covered) or "generic".
 
     Inputs that require grad get gradients from the library's backward
     (``sa_prefill_bwd``: atomics-free, bitwise reproducible).  Deviation from

@@ -4,13 +4,14 @@
 // keys j).  Lane l holds row n = l % 32 and half h = l / 32.  Per 32-key chunk
 // of the long axis staged in LDS:
 //
-//   S^T = K_chunk · A^T     D/16 v_mfma_f32_32x32x16_bf16, K rows from LDS
+//   S^T = K_chunk · A^T     DK/16 v_mfma_f32_32x32x16_bf16, K rows from LDS
 //   P^T = exp2(S^T*c - m)   per-row online softmax, lazy rescale
-//   O^T += V^T · P^T        D/32 x 2 MFMAs; the V^T operand is read from the
+//   O^T += V^T · P^T        DV/32 x 2 MFMAs; the V^T operand is read from the
 //                           natural [key][d] tile with ds_read_b64_tr_b16
 //
-// LDS tiles: K and V, each [rows][D] bf16, row-major with a 32-byte pad per
-// row (see TileGeom).
+// DK is the score width (q, k1, k2) and DV the value width (v1, v2, out); the
+// reference's determinant scores use DK = 2 * DV.  LDS tiles: K [rows][DK]
+// and V [rows][DV] bf16, row-major with a 32-byte pad per row (see TileGeom).
 //
 // Tiles are filled with global_load_lds_dwordx4 (16 bytes per lane straight
 // into LDS, no staging registers); one instruction fills 1 KB of LDS.
@@ -29,37 +30,43 @@ typedef short shortx8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
 
-// LDS tile geometry.  K and V tiles are [rows][D] bf16 with a row stride of
-// 2D + 32 bytes: the 32-byte pad shifts consecutive rows by 8 banks, which
-// keeps both the 16-byte K reads (32 rows, one segment) and the 8-byte
-// transposing V reads (4 rows x 32 bytes per 16 lanes) free of bank
-// conflicts, and every read address is a per-lane base plus an immediate.
-template <int D, int ROWS_T, int NW, int PAD = 32>
+// LDS tile geometry.  The K tile is [rows][DK] bf16 with a row stride of
+// 2DK + 32 bytes, the V tile [rows][DV] with 2DV + 32: the 32-byte pad shifts
+// consecutive rows by 8 banks, which keeps both the 16-byte K reads (32 rows,
+// one segment) and the 8-byte transposing V reads (4 rows x 32 bytes per 16
+// lanes) free of bank conflicts, and every read address is a per-lane base
+// plus an immediate.
+template <int DK, int DV, int ROWS_T, int NW, int PAD = 32>
 struct TileGeom {
-  static constexpr int kSegs = D / 8;                      // 16-byte segments per row
-  static constexpr int RS = 2 * D + PAD;                   // LDS row stride (bytes)
-  static constexpr int TB = ROWS_T * RS;                   // one tensor tile (bytes)
-  static constexpr int kTensorInstr = (TB + 1023) / 1024;  // DMA instructions per tensor tile
-  static constexpr int kInstr = (2 * kTensorInstr + NW - 1) / NW * NW;
-  static constexpr int NI = kInstr / NW;                   // DMA instructions per wave per tile
-  static constexpr int VOFF = kTensorInstr * 1024;         // V tile offset inside a slot
-  static constexpr int SLOT = kInstr * 1024;               // bytes of one ring slot
+  static constexpr int kSegsK = DK / 8;                       // 16-byte segments per K row
+  static constexpr int kSegsV = DV / 8;                       // ... per V row
+  static constexpr int RSK = 2 * DK + PAD;                    // LDS row strides (bytes)
+  static constexpr int RSV = 2 * DV + PAD;
+  static constexpr int TBK = ROWS_T * RSK;                    // one K tile (bytes)
+  static constexpr int TBV = ROWS_T * RSV;                    // one V tile
+  static constexpr int kInstrK = (TBK + 1023) / 1024;         // DMA instructions per K tile
+  static constexpr int kInstrV = (TBV + 1023) / 1024;         // ... per V tile
+  static constexpr int kInstr = (kInstrK + kInstrV + NW - 1) / NW * NW;
+  static constexpr int NI = kInstr / NW;                      // DMA instructions per wave per tile
+  static constexpr int VOFF = kInstrK * 1024;                 // V tile offset inside a slot
+  static constexpr int SLOT = kInstr * 1024;                  // bytes of one ring slot
 
   // DMA instruction k of wave `wid` fills LDS bytes [1024*(wid*NI + k), +1024)
-  // of the slot; instructions 0..kTensorInstr-1 fill the K tile, the next
-  // kTensorInstr the V tile, any further ones are idle (they re-fetch row 0
-  // into the unused tail).  Lane `lane` fetches row `row`, segment `seg` of
-  // tensor is_v.  Pad bytes fetch segment 0 of their row (never read).
+  // of the slot; instructions 0..kInstrK-1 fill the K tile, the next kInstrV
+  // the V tile, any further ones are idle (they re-fetch row 0 into the
+  // unused tail).  Lane `lane` fetches row `row`, segment `seg` of tensor
+  // is_v.  Pad bytes fetch segment 0 of their row (never read).
   __device__ static __forceinline__ void decode(int wid, int k, int lane, int& is_v, int& row, int& seg) {
     const int i = wid * NI + k;
-    is_v = i >= kTensorInstr;
-    int b = (is_v ? i - kTensorInstr : i) * 1024 + lane * 16;
-    if (i >= 2 * kTensorInstr || b >= TB) b = 0;
-    row = b / RS;
-    seg = (b % RS) >> 4;
-    if (seg >= kSegs) seg = 0;
+    is_v = i >= kInstrK;
+    const int tb = is_v ? TBV : TBK, rs = is_v ? RSV : RSK, segs = is_v ? kSegsV : kSegsK;
+    int b = (is_v ? i - kInstrK : i) * 1024 + lane * 16;
+    if (i >= kInstrK + kInstrV || b >= tb) b = 0;
+    row = b / rs;
+    seg = (b % rs) >> 4;
+    if (seg >= segs) seg = 0;
   }
-  __device__ static __forceinline__ bool instr_is_v(int wid, int k) { return wid * NI + k >= kTensorInstr; }
+  __device__ static __forceinline__ bool instr_is_v(int wid, int k) { return wid * NI + k >= kInstrK; }
   __device__ static __forceinline__ char* dst(char* slot, int wid, int k) { return slot + (wid * NI + k) * 1024; }
 };
 
@@ -153,16 +160,16 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 }
 
 // Per-wave state for 32 A rows.
-template <int D>
+template <int DK, int DV>
 struct RowBlock {
-  bf16x8 a[D / 16];     // A^T fragments (B operand of S^T = K·A^T)
-  floatx16 o[D / 32];   // O^T accumulators, d-block db holds d = 32*db + acc_row(r, half)
+  bf16x8 a[DK / 16];    // A^T fragments (B operand of S^T = K·A^T)
+  floatx16 o[DV / 32];  // O^T accumulators, d-block db holds d = 32*db + acc_row(r, half)
   float m;              // running max (log2 domain), identical in both halves
   float z;              // running sum of this lane's 16 keys per chunk (halves added at the end)
 
   __device__ __forceinline__ void reset() {
 #pragma unroll
-    for (int i = 0; i < D / 32; ++i) o[i] = floatx16{};
+    for (int i = 0; i < DV / 32; ++i) o[i] = floatx16{};
     m = kMInit;
     z = 0.f;
   }
@@ -171,16 +178,16 @@ struct RowBlock {
   // zero where `valid` is false (q_neg flips the sign of q, which keeps the
   // softmax scale non-negative).  Split in two so that callers can issue
   // other loads between the fragment loads and their first use: load_a
-  // reads the 2*D/16 fragments (q and k1 must point at readable rows in
+  // reads the 2*DK/16 fragments (q and k1 must point at readable rows in
   // every lane), make_a forms the bf16 products.
   struct AInputs {
-    bf16x8 q[D / 16], k[D / 16];
+    bf16x8 q[DK / 16], k[DK / 16];
   };
   __device__ static __forceinline__ AInputs load_a(const bf16* __restrict__ q, const bf16* __restrict__ k1,
                                                    int half) {
     AInputs in;
 #pragma unroll
-    for (int t = 0; t < D / 16; ++t) {
+    for (int t = 0; t < DK / 16; ++t) {
       const int d0 = 16 * t + 8 * half;
       in.q[t] = *(const bf16x8*)(q + d0);
       in.k[t] = *(const bf16x8*)(k1 + d0);
@@ -189,7 +196,7 @@ struct RowBlock {
   }
   __device__ __forceinline__ void make_a(const AInputs& in, bool valid, bool q_neg) {
 #pragma unroll
-    for (int t = 0; t < D / 16; ++t) {
+    for (int t = 0; t < DK / 16; ++t) {
       bf16x8 r;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
@@ -204,12 +211,12 @@ struct RowBlock {
     make_a(load_a(q, k1, half), valid, q_neg);
   }
   // The same from rows staged in LDS: krow = the lane's k1 row, qrow = the
-  // wave's q row (both D contiguous bf16).
+  // wave's q row (both DK contiguous bf16).
   // Fragments are read in groups of 4 (bounded register footprint).
   __device__ __forceinline__ void form_a_lds(const char* krow, const char* qrow, bool valid, int half, bool q_neg) {
-    constexpr int GRP = D / 16 < 4 ? D / 16 : 4;
+    constexpr int GRP = DK / 16 < 4 ? DK / 16 : 4;
 #pragma unroll
-    for (int t0 = 0; t0 < D / 16; t0 += GRP) {
+    for (int t0 = 0; t0 < DK / 16; t0 += GRP) {
       bf16x8 qv[GRP], kv[GRP];
 #pragma unroll
       for (int u = 0; u < GRP; ++u) {
@@ -230,35 +237,35 @@ struct RowBlock {
     }
   }
 
-  // The two transposing reads of V fragment `step` (t = step / (D/32) selects
-  // keys 16t.., db = step % (D/32) the 32-wide d block).
+  // The two transposing reads of V fragment `step` (t = step / (DV/32) selects
+  // keys 16t.., db = step % (DV/32) the 32-wide d block).
   template <int RS, int STEP>
   __device__ static __forceinline__ void vread(uint32_t vp, shortx4& v1, shortx4& v2) {
-    constexpr int t = STEP / (D / 32), db = STEP % (D / 32);
+    constexpr int t = STEP / (DV / 32), db = STEP % (DV / 32);
     constexpr int off = 16 * t * RS + 64 * db;
     v1 = ds_read_tr16<off>(vp);
     v2 = ds_read_tr16<off + 8 * RS>(vp);
   }
 
-  // One 32-key chunk: tile rows row0 .. row0+31 of the K tile at `ktile` and
-  // the V tile at `vtile` (row stride RS bytes).  sl2 = |scale|*log2(e) >= 0.
+  // One 32-key chunk: tile rows row0 .. row0+31 of the K tile at `ktile` (row
+  // stride RSK bytes) and the V tile at `vtile` (row stride RSV).  sl2 = |scale|*log2(e) >= 0.
   // key_lo/key_hi: range of valid chunk keys (0..31) for this wave's query;
   // masking is applied only when the chunk is not fully valid.
-  template <int RS>
+  template <int RSK, int RSV>
   __device__ __forceinline__ void chunk(const char* ktile, const char* vtile, int row0, int lane, float sl2,
                                         int key_lo, int key_hi) {
     const int n = lane & 31, half = lane >> 5;
     floatx16 s = floatx16{};
     {
       // K fragments are read one step ahead of their MFMA; the scheduling
-      // barriers stop the compiler from hoisting all D/16 reads (which would
-      // hold D/4 extra VGPRs live).
-      const char* kp = ktile + (row0 + n) * RS + 16 * half;
+      // barriers stop the compiler from hoisting all DK/16 reads (which would
+      // hold DK/4 extra VGPRs live).
+      const char* kp = ktile + (row0 + n) * RSK + 16 * half;
       bf16x8 kf = *(const bf16x8*)kp;
 #pragma unroll
-      for (int t = 0; t < D / 16; ++t) {
+      for (int t = 0; t < DK / 16; ++t) {
         bf16x8 kn;
-        if (t + 1 < D / 16) kn = *(const bf16x8*)(kp + 32 * (t + 1));
+        if (t + 1 < DK / 16) kn = *(const bf16x8*)(kp + 32 * (t + 1));
         __builtin_amdgcn_sched_barrier(0);
         s = mfma32x32x16(kf, a[t], s);
         __builtin_amdgcn_sched_barrier(0);
@@ -289,7 +296,7 @@ struct RowBlock {
       const float mn = fmaxf(m, cand);
       const float alpha = fast_exp2(m - mn);
 #pragma unroll
-      for (int i = 0; i < D / 32; ++i) o[i] *= alpha;
+      for (int i = 0; i < DV / 32; ++i) o[i] *= alpha;
       z *= alpha;
       m = mn;
     }
@@ -321,20 +328,20 @@ struct RowBlock {
     // and keys 16t + 4*half + {0..3} (+8 for the second read).
     const int g16 = (lane >> 4) & 1, i16 = lane & 15;
     const int e_src = i16 >> 2, q_src = i16 & 3;
-    const uint32_t vp = lds_addr(vtile + (row0 + 4 * half + e_src) * RS + 32 * g16 + 8 * q_src);
+    const uint32_t vp = lds_addr(vtile + (row0 + 4 * half + e_src) * RSV + 32 * g16 + 8 * q_src);
     // V fragments are read one step ahead of their MFMA
-    constexpr int kSteps = 2 * (D / 32);
+    constexpr int kSteps = 2 * (DV / 32);
     shortx4 v1, v2;
-    vread<RS, 0>(vp, v1, v2);
+    vread<RSV, 0>(vp, v1, v2);
     lds_wait(v1, v2);
     static_for<0, kSteps>([&](auto st) {
       constexpr int step = decltype(st)::value;
       shortx8 vv = {v1[0], v1[1], v1[2], v1[3], v2[0], v2[1], v2[2], v2[3]};
       const bf16x8 vf = __builtin_bit_cast(bf16x8, vv);
       shortx4 n1, n2;
-      if constexpr (step + 1 < kSteps) vread<RS, step + 1>(vp, n1, n2);
+      if constexpr (step + 1 < kSteps) vread<RSV, step + 1>(vp, n1, n2);
       __builtin_amdgcn_sched_barrier(0);
-      o[step % (D / 32)] = mfma32x32x16(vf, pb[step / (D / 32)], o[step % (D / 32)]);
+      o[step % (DV / 32)] = mfma32x32x16(vf, pb[step / (DV / 32)], o[step % (DV / 32)]);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (step + 1 < kSteps) {
         lds_wait(n1, n2);
@@ -353,13 +360,13 @@ struct RowBlock {
   // work of a wave issues while its own MFMAs occupy the matrix core.
 
   // Raw scores of one chunk (pipeline prologue; no interleaving).
-  template <int RS>
+  template <int RSK>
   __device__ __forceinline__ floatx16 qk(const char* ktile, int row0, int lane) const {
     const int n = lane & 31, half = lane >> 5;
-    const char* kp = ktile + (row0 + n) * RS + 16 * half;
+    const char* kp = ktile + (row0 + n) * RSK + 16 * half;
     floatx16 s = floatx16{};
 #pragma unroll
-    for (int t = 0; t < D / 16; ++t) s = mfma32x32x16(*(const bf16x8*)(kp + 32 * t), a[t], s);
+    for (int t = 0; t < DK / 16; ++t) s = mfma32x32x16(*(const bf16x8*)(kp + 32 * t), a[t], s);
     return s;
   }
 
@@ -390,7 +397,7 @@ struct RowBlock {
       const float mn = fmaxf(m, cmax);
       const float alpha = fast_exp2(m - mn);
 #pragma unroll
-      for (int i = 0; i < D / 32; ++i) o[i] *= alpha;
+      for (int i = 0; i < DV / 32; ++i) o[i] *= alpha;
       z *= alpha;
       m = mn;
     }
@@ -400,11 +407,12 @@ struct RowBlock {
   // the rescale for chunk c has been applied.  With NEXT, the QK^T of chunk
   // c+1 (K tile `knext`) is computed into `s` and its scaled row max into
   // `cmax`.  `vtile` is chunk c's V tile; both tiles use rows row0.. .
-  template <int RS, bool NEXT>
+  template <int RSK, int RSV, bool NEXT>
   __device__ __forceinline__ void step(floatx16& s, float& cmax, const char* knext, const char* vtile, int row0,
                                        int lane, float sl2) {
+    static_assert(DK <= 128 && DV <= 128, "the pipelined step covers score and value widths up to 128");
     const int n = lane & 31, half = lane >> 5;
-    constexpr int NT = D / 16;   // QK^T MFMAs
+    constexpr int NT = DK / 16;   // QK^T MFMAs
     constexpr int PER = 16 / NT; // probabilities per QK^T MFMA (2 or 4)
     floatx16 sn = floatx16{};
     uint32_t pk[8];              // P^T as packed bf16 pairs (B operand of the PV MFMAs)
@@ -413,13 +421,13 @@ struct RowBlock {
     // V^T operand addresses (see vread); the first pair is issued now
     const int g16 = (lane >> 4) & 1, i16 = lane & 15;
     const int e_src = i16 >> 2, q_src = i16 & 3;
-    const uint32_t vp = lds_addr(vtile + (row0 + 4 * half + e_src) * RS + 32 * g16 + 8 * q_src);
-    constexpr int kSteps = 2 * (D / 32);
+    const uint32_t vp = lds_addr(vtile + (row0 + 4 * half + e_src) * RSV + 32 * g16 + 8 * q_src);
+    constexpr int kSteps = 2 * (DV / 32);
     shortx4 v1, v2;
-    vread<RS, 0>(vp, v1, v2);
+    vread<RSV, 0>(vp, v1, v2);
 
     // phase 1
-    const char* kp = knext + (row0 + n) * RS + 16 * half;
+    const char* kp = knext + (row0 + n) * RSK + 16 * half;
     bf16x8 kf;
     if constexpr (NEXT) kf = *(const bf16x8*)kp;
     static_for<0, NT>([&](auto tt) {
@@ -454,9 +462,9 @@ struct RowBlock {
       shortx8 vv = {v1[0], v1[1], v1[2], v1[3], v2[0], v2[1], v2[2], v2[3]};
       const bf16x8 vf = __builtin_bit_cast(bf16x8, vv);
       shortx4 n1, n2;
-      if constexpr (step + 1 < kSteps) vread<RS, step + 1>(vp, n1, n2);
+      if constexpr (step + 1 < kSteps) vread<RSV, step + 1>(vp, n1, n2);
       __builtin_amdgcn_sched_barrier(0);
-      o[step % (D / 32)] = mfma32x32x16(vf, step / (D / 32) == 0 ? pb0 : pb1, o[step % (D / 32)]);
+      o[step % (DV / 32)] = mfma32x32x16(vf, step / (DV / 32) == 0 ? pb0 : pb1, o[step % (DV / 32)]);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (NEXT) {
 #pragma unroll

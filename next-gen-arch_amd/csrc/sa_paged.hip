@@ -59,7 +59,8 @@ constexpr int kPosCache = 1024;  // long-window positions of one split whose row
 
 template <int D, int NW, int P>
 __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel(PagedParams p) {
-  using G = TileGeom<D, kChunk, NW>;
+  using G = TileGeom<D, D, kChunk, NW>;
+  using RB = RowBlock<D, D>;
   constexpr bool kPipelined = D <= 128 && P >= 2;  // second score tile fits the registers up to D = 128
   constexpr int SLOT = G::SLOT;
   constexpr int R = P + 1;
@@ -103,7 +104,7 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
   const int cbeg = cfirst + split * per;
   const int cend = min(p.nc, cbeg + per);
 
-  RowBlock<D> rb;
+  RB rb;
   const int j = pos - 32 * r - n;
   const bool row_ok = task_ok && j >= lo1 && cbeg < cend;
 
@@ -205,8 +206,8 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
       // of chunk c+1 and V of chunk c
       wait_tiles<NI, P>(min(P - 1, cend - 1 - cbeg));
       block_barrier();
-      floatx16 s = rb.template qk<G::RS>(lds + (cbeg % R) * SLOT, 0, lane);
-      float cmax = RowBlock<D>::row_max(s) * p.sl2;
+      floatx16 s = rb.template qk<G::RSK>(lds + (cbeg % R) * SLOT, 0, lane);
+      float cmax = RB::row_max(s) * p.sl2;
       auto begin_chunk = [&](int c) {
         block_barrier();
         if (c + P < cend) issue(c + P);
@@ -214,8 +215,8 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
         const int klo = task_ok ? max(lo2 - kfirst, 0) : kChunk;
         const int khi = task_ok ? min(pos - kfirst, kChunk - 1) : -1;
         if (klo > 0 || khi < kChunk - 1) {  // edge chunk (uniform branch)
-          RowBlock<D>::mask(s, lane, klo, khi);
-          cmax = RowBlock<D>::row_max(s) * p.sl2;
+          RB::mask(s, lane, klo, khi);
+          cmax = RB::row_max(s) * p.sl2;
         }
         rb.rescale(cmax);
       };
@@ -224,11 +225,11 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
         wait_tiles<NI, P>(min(P - 2, cend - 2 - c));
         begin_chunk(c);
         const char* slot = lds + (c % R) * SLOT;
-        rb.template step<G::RS, true>(s, cmax, lds + ((c + 1) % R) * SLOT, slot + G::VOFF, 0, lane, p.sl2);
+        rb.template step<G::RSK, G::RSV, true>(s, cmax, lds + ((c + 1) % R) * SLOT, slot + G::VOFF, 0, lane, p.sl2);
       }
       begin_chunk(c);
       const char* slot = lds + (c % R) * SLOT;
-      rb.template step<G::RS, false>(s, cmax, slot, slot + G::VOFF, 0, lane, p.sl2);
+      rb.template step<G::RSK, G::RSV, false>(s, cmax, slot, slot + G::VOFF, 0, lane, p.sl2);
     } else {
       for (int c = cbeg; c < cend; ++c) {
         wait_tiles<NI, P>(min(P - 1, cend - 1 - c));
@@ -237,7 +238,7 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
         // unconditional (see the prefill kernel): idle waves get an empty key range
         const int kfirst = kstart + kChunk * c;
         const char* slot = lds + (c % R) * SLOT;
-        rb.template chunk<G::RS>(slot, slot + G::VOFF, 0, lane, p.sl2, task_ok ? max(lo2 - kfirst, 0) : kChunk,
+        rb.template chunk<G::RSK, G::RSV>(slot, slot + G::VOFF, 0, lane, p.sl2, task_ok ? max(lo2 - kfirst, 0) : kChunk,
                                  task_ok ? min(pos - kfirst, kChunk - 1) : -1);
       }
     }
@@ -429,7 +430,7 @@ constexpr int kPagedDepth = SA_PAGED_DEPTH;  // tiles in flight per workgroup (2
 template <int D, int NW>
 static hipError_t launch_paged_mfma_t(PagedParams p, hipStream_t stream) {
   constexpr int P = D >= 256 ? 2 : kPagedDepth;
-  const size_t lds_ring = (size_t)(P + 1) * TileGeom<D, kChunk, NW>::SLOT + kPosCache * sizeof(int64_t);
+  const size_t lds_ring = (size_t)(P + 1) * TileGeom<D, D, kChunk, NW>::SLOT + kPosCache * sizeof(int64_t);
   const size_t lds_red = (size_t)NW * 64 * 36 * sizeof(float);
   const size_t lds = lds_ring > lds_red ? lds_ring : lds_red;
   auto kern = paged_mfma_kernel<D, NW, P>;

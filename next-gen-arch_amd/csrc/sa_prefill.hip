@@ -3,8 +3,9 @@
 // (archlab/architectures/simplicial_kernels.py:16-52) behind
 // simplicial_attention (simplicial_attention.py:77-97).
 //
-// bf16 MFMA kernel (D in {64, 128, 256}, DV == D)
-// ------------------------------------------------
+// bf16 MFMA kernel (score width DK, value width DV: DK == DV in {64, 128, 256},
+// or DK == 2 DV in {128, 256}, the determinant-score expansion)
+// ------------------------------------------------------------------------------
 // A workgroup of 4 waves owns NQ consecutive query tokens t0 .. t0+NQ-1 and
 // NH query heads of one KV group (NQ * NH == 4).  Wave w handles token
 // t0 + w / NH, head w % NH: its 32 A rows a_j = bf16(q_t ⊙ k1_j).  Every query
@@ -83,17 +84,19 @@ __device__ __forceinline__ int xcd_remap(int b, int n) {
 #define SA_PREFILL_WAVES 4
 #endif
 
-template <int D, int NQ, int NH, int P>
-__global__ __launch_bounds__(64 * NQ * NH, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_SIMD)) void prefill_mfma_kernel(PrefillParams p) {
+template <int DK, int DV, int NQ, int NH, int P>
+__global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREFILL_WAVES_PER_SIMD)) void prefill_mfma_kernel(
+    PrefillParams p) {
   static_assert(NQ * NH == 4 || NQ * NH == 8, "4 or 8 waves per block");
   static_assert(P >= 1 && P <= 4, "prefetch depth");
   constexpr int NW = NQ * NH;
   constexpr int ROWS = kChunk + NQ - 1;  // tile rows: one chunk of all NQ queries
-  using G = TileGeom<D, ROWS, NW>;
+  using G = TileGeom<DK, DV, ROWS, NW>;
+  static_assert(NW * G::RSK <= G::kInstrV * 1024, "the q rows fit the short slot's V region");
   constexpr int R = P + 1;  // ring slots for the long-axis tiles
   constexpr int NI = G::NI;
-  // the pipelined loop holds a second score tile: registers allow it up to D = 128
-  constexpr bool kPipelined = D <= 128 && P >= 2;
+  // the pipelined loop holds a second score tile: registers allow it up to DK = DV = 128
+  constexpr bool kPipelined = DK <= 128 && DV <= 128 && P >= 2;
   extern __shared__ __attribute__((aligned(16))) char lds[];
   // One more slot after the ring holds the short window of the pass: its K
   // region takes the k1 rows and (in its V region) the q rows of the NW waves
@@ -181,12 +184,12 @@ __global__ __launch_bounds__(64 * NQ * NH, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_
   // q rows of the NW waves into rows 0..NW-1 of the short slot's V region (wave 0)
   auto dma_q = [&]() {
     if (wid == 0) {
-      constexpr int QI = (NW * G::RS + 1023) / 1024;
+      constexpr int QI = (NW * G::RSK + 1023) / 1024;
 #pragma unroll
       for (int k = 0; k < QI; ++k) {
         const int b = k * 1024 + lane * 16;
-        int row = b / G::RS, seg = (b % G::RS) >> 4;
-        if (row >= NW || seg >= G::kSegs) row = 0, seg = 0;
+        int row = b / G::RSK, seg = (b % G::RSK) >> 4;
+        if (row >= NW || seg >= G::kSegsK) row = 0, seg = 0;
         const int tq = min(t0 + row / NH, last);
         const int hq = g * p.group + hs * NH + row % NH;
         dma16(p.q + (int64_t)tq * p.q_st + (int64_t)hq * p.q_sh + seg * 8, sslot + G::VOFF + k * 1024);
@@ -195,12 +198,13 @@ __global__ __launch_bounds__(64 * NQ * NH, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_
   };
 
   const int half = lane >> 5, n = lane & 31;
-  RowBlock<D> rb;
+  using RB = RowBlock<DK, DV>;
+  RB rb;
   // Running merge over the row-group passes: out values for d = 64*i + lane,
   // plus (M, Z) in the log2 domain.
-  float orun[D / 64];
+  float orun[DV / 64];
 #pragma unroll
-  for (int i = 0; i < D / 64; ++i) orun[i] = 0.f;
+  for (int i = 0; i < DV / 64; ++i) orun[i] = 0.f;
   float Mrun = -INFINITY, Zrun = 0.f;
 
   for (int r = 0; r < p.nr; ++r) {
@@ -216,7 +220,7 @@ __global__ __launch_bounds__(64 * NQ * NH, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_
     wait_vmcnt<P * NI>();
     block_barrier();
     const int srow = qo + 31 - n;  // this lane's short key j in the short slot
-    rb.form_a_lds(sslot + srow * G::RS, sslot + G::VOFF + wid * G::RS, row_ok, half, p.q_neg != 0);
+    rb.form_a_lds(sslot + srow * G::RSK, sslot + G::VOFF + wid * G::RSK, row_ok, half, p.q_neg != 0);
     rb.reset();
     if constexpr (kPipelined) {
       // Software-pipelined chunk loop: iteration c needs K of chunk c+1 and
@@ -225,8 +229,8 @@ __global__ __launch_bounds__(64 * NQ * NH, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_
       if (c0 < p.nc) {
         wait_tiles<NI, P>(min(P - 1, p.nc - 1 - c0));
         block_barrier();
-        floatx16 s = rb.template qk<G::RS>(lds + (c0 % R) * G::SLOT, qo, lane);
-        float cmax = RowBlock<D>::row_max(s) * p.sl2;
+        floatx16 s = rb.template qk<G::RSK>(lds + (c0 % R) * G::SLOT, qo, lane);
+        float cmax = RB::row_max(s) * p.sl2;
         // the last chunk (no successor) is peeled off so that the loop body
         // has a single definition of the accumulators
         auto begin_chunk = [&](int c, floatx16& sc, float& cm) {
@@ -237,8 +241,8 @@ __global__ __launch_bounds__(64 * NQ * NH, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_
           const int klo = active ? max(lo2 - kfirst, 0) : kChunk;
           const int khi = active ? min(t - kfirst, kChunk - 1) : -1;
           if (klo > 0 || khi < kChunk - 1) {  // edge chunk (uniform branch)
-            RowBlock<D>::mask(sc, lane, klo, khi);
-            cm = RowBlock<D>::row_max(sc) * p.sl2;
+            RB::mask(sc, lane, klo, khi);
+            cm = RB::row_max(sc) * p.sl2;
           }
           rb.rescale(cm);
         };
@@ -247,12 +251,13 @@ __global__ __launch_bounds__(64 * NQ * NH, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_
           wait_tiles<NI, P>(min(P - 2, p.nc - 2 - c));
           begin_chunk(c, s, cmax);
           const char* slot = lds + (c % R) * G::SLOT;
-          rb.template step<G::RS, true>(s, cmax, lds + ((c + 1) % R) * G::SLOT, slot + G::VOFF, qo, lane, p.sl2);
+          rb.template step<G::RSK, G::RSV, true>(s, cmax, lds + ((c + 1) % R) * G::SLOT, slot + G::VOFF, qo, lane,
+                                                 p.sl2);
         }
         begin_chunk(c, s, cmax);
         dma_tile(std::integral_constant<int, 2>{}, sslot, kbs, p.k1, p.v1);  // v1 rows for the epilogue
         const char* slot = lds + (c % R) * G::SLOT;
-        rb.template step<G::RS, false>(s, cmax, slot, slot + G::VOFF, qo, lane, p.sl2);
+        rb.template step<G::RSK, G::RSV, false>(s, cmax, slot, slot + G::VOFF, qo, lane, p.sl2);
       } else {
         dma_tile(std::integral_constant<int, 2>{}, sslot, kbs, p.k1, p.v1);
       }
@@ -269,8 +274,9 @@ __global__ __launch_bounds__(64 * NQ * NH, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_
         const bool active = qvalid && c >= cfirst;
         const int kfirst = t - p.wl + 1 + kChunk * c;  // key of this wave's chunk row 0
         const char* slot = lds + (c % R) * G::SLOT;
-        rb.template chunk<G::RS>(slot, slot + G::VOFF, qo, lane, p.sl2, active ? max(lo2 - kfirst, 0) : kChunk,
-                                 active ? min(t - kfirst, kChunk - 1) : -1);
+        rb.template chunk<G::RSK, G::RSV>(slot, slot + G::VOFF, qo, lane, p.sl2,
+                                          active ? max(lo2 - kfirst, 0) : kChunk,
+                                          active ? min(t - kfirst, kChunk - 1) : -1);
       }
       if (c0 >= p.nc) dma_tile(std::integral_constant<int, 2>{}, sslot, kbs, p.k1, p.v1);
     }
@@ -284,12 +290,12 @@ __global__ __launch_bounds__(64 * NQ * NH, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_
     const float wgt = (row_ok && Mw > -INFINITY) ? fast_exp2(mrow - Mw) : 0.f;
     const float Zw = half_sum(wgt * zrow);
     float* red = (float*)lds + wid * (64 * 36);  // [64 d][36] per wave (ring region)
-    const char* v1s = sslot + G::VOFF + srow * G::RS;  // this lane's v1 row
+    const char* v1s = sslot + G::VOFF + srow * G::RSV;  // this lane's v1 row
     const float Mn = fmaxf(Mrun, Mw);
     const float a0 = Mrun > -INFINITY ? fast_exp2(Mrun - Mn) : 0.f;
     const float a1 = Mw > -INFINITY ? fast_exp2(Mw - Mn) : 0.f;
 #pragma unroll
-    for (int sl = 0; sl < D / 64; ++sl) {
+    for (int sl = 0; sl < DV / 64; ++sl) {
 #pragma unroll
       for (int dbl = 0; dbl < 2; ++dbl) {
         const int db = 2 * sl + dbl;
@@ -321,7 +327,7 @@ __global__ __launch_bounds__(64 * NQ * NH, (D >= 256 ? 1 : SA_PREFILL_WAVES_PER_
     const float inv = 1.f / Zrun;
     bf16* orow = p.out + (int64_t)t * p.o_st + (int64_t)h * p.o_sh;
 #pragma unroll
-    for (int i = 0; i < D / 64; ++i) orow[64 * i + lane] = (bf16)(orun[i] * inv);
+    for (int i = 0; i < DV / 64; ++i) orow[64 * i + lane] = (bf16)(orun[i] * inv);
     if (p.lse && lane == 0) p.lse[(int64_t)t * p.lse_st + h] = (Mrun + __log2f(Zrun)) * kLn2;
   }
 }
@@ -344,18 +350,18 @@ __global__ __launch_bounds__(kGenThreads) void prefill_generic_kernel(GenericPre
 // ---------------------------------------------------------------------------
 // Host launchers
 
-template <int D, int NQ, int NH, int P>
+template <int DK, int DV, int NQ, int NH, int P>
 static hipError_t launch_prefill_mfma(const PrefillParams& base_p, hipStream_t stream) {
   PrefillParams p = base_p;
   p.qblocks = (p.total + NQ - 1) / NQ;
   p.hsub = p.group / NH;
   p.nblocks = p.qblocks * p.hk * p.hsub;
   constexpr int NW = NQ * NH;
-  using G = TileGeom<D, kChunk + NQ - 1, NW>;
+  using G = TileGeom<DK, DV, kChunk + NQ - 1, NW>;
   size_t lds = (size_t)(P + 2) * G::SLOT;  // P + 1 ring slots + the short-window slot
   const size_t red = (size_t)NW * 64 * 36 * sizeof(float);
   if (lds < red) lds = red;
-  auto kern = prefill_mfma_kernel<D, NQ, NH, P>;
+  auto kern = prefill_mfma_kernel<DK, DV, NQ, NH, P>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(p.nblocks), dim3(64 * NW), lds, stream, p);
@@ -364,23 +370,23 @@ static hipError_t launch_prefill_mfma(const PrefillParams& base_p, hipStream_t s
 
 // Prefetch depth per configuration: the ring is sized to leave room for two
 // workgroups per CU (<= 80 KB) where registers allow it.
-template <int D>
+template <int DK, int DV>
 static hipError_t dispatch_prefill_mfma_d(const PrefillParams& p, hipStream_t stream) {
   const int G = p.group;
-  if constexpr (D >= 256) {
-    if (G % 4 == 0) return launch_prefill_mfma<D, 1, 4, 2>(p, stream);
-    if (G % 2 == 0) return launch_prefill_mfma<D, 2, 2, 2>(p, stream);
-    return launch_prefill_mfma<D, 4, 1, 2>(p, stream);
+  if constexpr (DK >= 256 || DV >= 256) {
+    if (G % 4 == 0) return launch_prefill_mfma<DK, DV, 1, 4, 2>(p, stream);
+    if (G % 2 == 0) return launch_prefill_mfma<DK, DV, 2, 2, 2>(p, stream);
+    return launch_prefill_mfma<DK, DV, 4, 1, 2>(p, stream);
   } else if constexpr (SA_PREFILL_WAVES == 8) {
     // one 8-wave workgroup per CU: a tile serves twice the queries
-    if (G % 4 == 0) return launch_prefill_mfma<D, 2, 4, 3>(p, stream);
-    if (G % 2 == 0) return launch_prefill_mfma<D, 4, 2, 3>(p, stream);
-    return launch_prefill_mfma<D, 8, 1, 3>(p, stream);
+    if (G % 4 == 0) return launch_prefill_mfma<DK, DV, 2, 4, 3>(p, stream);
+    if (G % 2 == 0) return launch_prefill_mfma<DK, DV, 4, 2, 3>(p, stream);
+    return launch_prefill_mfma<DK, DV, 8, 1, 3>(p, stream);
   } else {
     constexpr int P = SA_PREFILL_DEPTH;
-    if (G % 4 == 0) return launch_prefill_mfma<D, 1, 4, P>(p, stream);
-    if (G % 2 == 0) return launch_prefill_mfma<D, 2, 2, P>(p, stream);
-    return launch_prefill_mfma<D, 4, 1, P>(p, stream);
+    if (G % 4 == 0) return launch_prefill_mfma<DK, DV, 1, 4, P>(p, stream);
+    if (G % 2 == 0) return launch_prefill_mfma<DK, DV, 2, 2, P>(p, stream);
+    return launch_prefill_mfma<DK, DV, 4, 1, P>(p, stream);
   }
 }
 
@@ -416,12 +422,18 @@ hipError_t launch_prefill_bf16_mfma(const sa_prefill_args* a, hipStream_t stream
   // > 0 even for scale == 0, so that a masked score (-inf) maps to p = 0
   p.sl2 = fmaxf(fabsf(a->scale) * kLog2e, 1e-30f);
   p.q_neg = a->scale < 0.f;
-  switch (a->head_dim) {
-    case 64: return dispatch_prefill_mfma_d<64>(p, stream);
-    case 128: return dispatch_prefill_mfma_d<128>(p, stream);
-    case 256: return dispatch_prefill_mfma_d<256>(p, stream);
-    default: return hipErrorInvalidValue;
+  const int dk = a->head_dim, dv = a->value_dim;
+  if (dk == dv) {
+    switch (dk) {
+      case 64: return dispatch_prefill_mfma_d<64, 64>(p, stream);
+      case 128: return dispatch_prefill_mfma_d<128, 128>(p, stream);
+      case 256: return dispatch_prefill_mfma_d<256, 256>(p, stream);
+      default: return hipErrorInvalidValue;
+    }
   }
+  if (dk == 128 && dv == 64) return dispatch_prefill_mfma_d<128, 64>(p, stream);
+  if (dk == 256 && dv == 128) return dispatch_prefill_mfma_d<256, 128>(p, stream);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_prefill_generic(const sa_prefill_args* a, hipStream_t stream) {

@@ -105,6 +105,31 @@ def test_mfma_window_edges(cuda, ws, wl):
     _check(cuda, 1, 300, 4, 2, 128, ws, wl, torch.bfloat16, seed=ws * 7 + wl, kernel="mfma")
 
 
+@pytest.mark.parametrize("d,dv", [(128, 64), (256, 128)])
+@pytest.mark.parametrize("hq,hk", [(4, 4), (8, 2), (3, 1)])
+def test_mfma_score_and_value_widths_differ(cuda, d, dv, hq, hk):
+    """Score width DK != value width DV (the determinant expansion's DK = 2 DV) on the MFMA kernel."""
+    _check(cuda, 2, 150, hq, hk, d, 16, 64, torch.bfloat16, seed=d + dv + hq, kernel="mfma", dv=dv)
+
+
+@pytest.mark.parametrize("ws,wl", [(1, 1), (33, 100), (5, 300)])
+def test_mfma_score_and_value_widths_differ_windows(cuda, ws, wl):
+    _check(cuda, 1, 320, 4, 2, 128, ws, wl, torch.bfloat16, seed=ws + wl, kernel="mfma", dv=64)
+    _check(cuda, 1, 200, 8, 2, 256, ws, wl, torch.bfloat16, seed=ws + wl + 1, kernel="mfma", dv=128)
+
+
+def test_mfma_score_and_value_widths_differ_varlen(cuda):
+    _, varlen, _ = _api()
+    lengths = [3, 140, 61]
+    cu = torch.tensor([0, 3, 143, 204], dtype=torch.int32)
+    x = rand_inputs(1, sum(lengths), 8, 2, 256, dv=128, seed=31)
+    out, lse = varlen(*(v[0].to(cuda) for v in x), cu.to(cuda), 40, 96, scale=1.0, return_lse=True,
+                      kernel="mfma")
+    ref_o, ref_l = O.varlen_reference(*(v[0].float() for v in x), cu, 40, 96, scale=1.0, return_lse=True)
+    assert_out_close(out, ref_o, torch.bfloat16)
+    assert_lse_close(lse, ref_l, torch.bfloat16, rtol=1e-2)
+
+
 def test_mfma_production_windows(cuda):
     """Reference production geometry: short 32, long 512, GQA 4, positions across both edges."""
     pos = [0, 1, 30, 31, 32, 33, 100, 510, 511, 512, 513, 700, 1023, 1100, 1199]
