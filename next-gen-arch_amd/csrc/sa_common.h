@@ -72,29 +72,48 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// xor-shuffle within groups of 32 lanes (ds_swizzle bit-mask mode, no
-// address registers): lane l reads lane l ^ m, m < 32.
-template <int M>
-__device__ __forceinline__ float swz_xor(float x) {
-  static_assert(M > 0 && M < 32, "xor mask within 32 lanes");
-  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x1f | (M << 10)));
+// Data-parallel-primitive moves (VALU only, no LDS round trip): lane l reads
+// lane quad_perm / mirror partner within its row of 16 lanes.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <- 7 - i within each 8 lanes
+constexpr int kDppMirror = 0x140;     // lane i <- 15 - i within each 16 lanes
+
+// The two 16-lane rows of each half exchanged with v_permlane16_swap (both
+// operands = x): every lane gets {x[l % 16 + 32*(l/32)], x[l % 16 + 16 + 32*(l/32)]}
+// in the same order, so combining them is bit-identical across the half.
+__device__ __forceinline__ float row_pair_max(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float row_pair_sum(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Max / sum over the 32 lanes that share l / 32.
+// Max / sum over the 32 lanes that share l / 32: butterflies inside quads,
+// then mirrors inside 8 and 16 lanes (each lane pairs with a lane of the
+// other group, so every lane holds the group result), then the row swap.
+// Each combining step is commutative in its two operands, so all 32 lanes
+// end with the same bits.
 __device__ __forceinline__ float half_max(float x) {
-  x = fmaxf(x, swz_xor<16>(x));
-  x = fmaxf(x, swz_xor<8>(x));
-  x = fmaxf(x, swz_xor<4>(x));
-  x = fmaxf(x, swz_xor<2>(x));
-  return fmaxf(x, swz_xor<1>(x));
+  x = fmaxf(x, dpp_mov<kDppXor1>(x));
+  x = fmaxf(x, dpp_mov<kDppXor2>(x));
+  x = fmaxf(x, dpp_mov<kDppHalfMirror>(x));
+  x = fmaxf(x, dpp_mov<kDppMirror>(x));
+  return row_pair_max(x);
 }
 
 __device__ __forceinline__ float half_sum(float x) {
-  x += swz_xor<16>(x);
-  x += swz_xor<8>(x);
-  x += swz_xor<4>(x);
-  x += swz_xor<2>(x);
-  return x + swz_xor<1>(x);
+  x += dpp_mov<kDppXor1>(x);
+  x += dpp_mov<kDppXor2>(x);
+  x += dpp_mov<kDppHalfMirror>(x);
+  x += dpp_mov<kDppMirror>(x);
+  return row_pair_sum(x);
 }
 
 __device__ __forceinline__ float wave_max(float x) { return pair_max(half_max(x)); }

@@ -294,6 +294,16 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
     const float Mn = fmaxf(Mrun, Mw);
     const float a0 = Mrun > -INFINITY ? fast_exp2(Mrun - Mn) : 0.f;
     const float a1 = Mw > -INFINITY ? fast_exp2(Mw - Mn) : 0.f;
+    // every v1 read is issued before the first use (one LDS wait, not one per
+    // read); rows outside the window are zeroed by a select after the load
+    bf16x4 v1v[DV / 64][2][4];
+#pragma unroll
+    for (int sl = 0; sl < DV / 64; ++sl)
+#pragma unroll
+      for (int dbl = 0; dbl < 2; ++dbl)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4)
+          v1v[sl][dbl][q4] = *(const bf16x4*)(v1s + 2 * (64 * sl + 32 * dbl + 8 * q4 + 4 * half));
 #pragma unroll
     for (int sl = 0; sl < DV / 64; ++sl) {
 #pragma unroll
@@ -302,9 +312,11 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
           const int dd = 32 * dbl + 8 * q4 + 4 * half;  // first of 4 consecutive d
-          const bf16x4 vv = row_ok ? *(const bf16x4*)(v1s + 2 * (64 * sl + dd)) : bf16x4{};
 #pragma unroll
-          for (int e = 0; e < 4; ++e) red[(dd + e) * 36 + n] = wgt * (float)vv[e] * rb.o[db][4 * q4 + e];
+          for (int e = 0; e < 4; ++e) {
+            const float v = row_ok ? (float)v1v[sl][dbl][q4][e] : 0.f;
+            red[(dd + e) * 36 + n] = wgt * v * rb.o[db][4 * q4 + e];
+          }
         }
       }
       // `red` is private to this wave and a wave's LDS accesses execute in
