@@ -113,7 +113,7 @@ def _prefill(q, k1, k2, v1, v2, short_window, long_window, scale, cu_seqlens, nu
 
 
 def _backward(q, k1, k2, v1, v2, out, lse, dout, dlse, short_window, long_window, scale, cu_seqlens, num_seqs,
-              seqlen):
+              seqlen, kernel="auto"):
     """Gradients of q, k1, k2, v1, v2 ([T,H,*] contiguous) through the C ABI."""
     lib = _native.load()
     tokens, hq, d = q.shape
@@ -130,7 +130,7 @@ def _backward(q, k1, k2, v1, v2, out, lse, dout, dlse, short_window, long_window
         lse_stride_t=hq, num_seqs=num_seqs, seqlen=seqlen, total_tokens=tokens,
         heads_q=hq, heads_kv=hk, head_dim=d, value_dim=dv,
         short_window=int(short_window), long_window=int(long_window), scale=scale,
-        dtype=_native.dtype_code(q.dtype), flags=0)
+        dtype=_native.dtype_code(q.dtype), flags=_kernel_flag(kernel))
     if dlse is not None:
         dlse = dlse.float().contiguous()
     args = _native.PrefillBwdArgs(
@@ -156,17 +156,17 @@ class _SimplicialFunction(torch.autograd.Function):
                             True, kernel)
         ctx.save_for_backward(q, k1, k2, v1, v2, out, lse)
         ctx.cu_seqlens = cu_seqlens
-        ctx.meta = (short_window, long_window, scale, num_seqs, seqlen)
+        ctx.meta = (short_window, long_window, scale, num_seqs, seqlen, kernel)
         return out, lse
 
     @staticmethod
     def backward(ctx, dout, dlse):
         q, k1, k2, v1, v2, out, lse = ctx.saved_tensors
-        short_window, long_window, scale, num_seqs, seqlen = ctx.meta
+        short_window, long_window, scale, num_seqs, seqlen, kernel = ctx.meta
         if dout is None:
             dout = torch.zeros_like(out)
         grads = _backward(q, k1, k2, v1, v2, out, lse, dout, dlse, short_window, long_window, scale,
-                          ctx.cu_seqlens, num_seqs, seqlen)
+                          ctx.cu_seqlens, num_seqs, seqlen, "generic" if kernel == "generic" else "auto")
         return (*grads, None, None, None, None, None, None, None)
 
 
@@ -193,7 +193,9 @@ def simplicial_attention(q, k1, k2, v1, v2, short_window, long_window, *, scale=
     (raise if not covered) or "generic".
 
     Inputs that require grad get gradients from the library's backward
-    (``sa_prefill_bwd``: atomics-free, bitwise reproducible).  Deviation from
+    (``sa_prefill_bwd``: atomics-free, bitwise reproducible; MFMA tiles for
+    bf16 with D == DV in {64, 128}, portable kernels otherwise and with
+    ``kernel="generic"``).  Deviation from
     the reference: forward and backward are deterministic, so
     ``torch.use_deterministic_algorithms(True)`` is allowed.
     """

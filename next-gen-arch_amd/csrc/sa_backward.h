@@ -1,0 +1,42 @@
+// Parameters shared by the backward kernels (portable: sa_backward.hip, MFMA:
+// sa_backward_mfma.hip).
+#pragma once
+
+#include "sa_common.h"
+
+namespace sa {
+
+struct BwdParams {
+  const void* q;
+  const void* k1;
+  const void* k2;
+  const void* v1;
+  const void* v2;
+  const void* out;
+  const float* lse;
+  const void* dout;
+  void* dq;
+  void* dk1;
+  void* dk2;
+  void* dv1;
+  void* dv2;
+  float* delta;  // [tokens, hq] workspace: dout·out - dlse
+  float* dl;     // [tokens, hq] workspace: dlse (0 without an LSE gradient)
+  const float* dlse;  // optional gradient of the LSE output
+  int64_t dlse_st;
+  const int32_t* cu;
+  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, lse_st;
+  int64_t do_st, do_sh, dq_st, dq_sh, dk_st, dk_sh, dv_st, dv_sh;
+  int tokens, seqlen, num_seqs, hq, hk, group, ws, wl, d, dv;
+  float scale;
+  int mfma;  // bf16 inputs and the MFMA passes allowed (not forced onto the portable kernels)
+};
+
+// MFMA passes (sa_backward_mfma.hip).  Each returns hipErrorNotSupported when
+// the call's shapes, dtype or strides are outside what its kernel covers; the
+// portable pass runs instead.
+hipError_t launch_bwd_dq_mfma(const BwdParams& p, hipStream_t stream);
+hipError_t launch_bwd_dkv1_mfma(const BwdParams& p, hipStream_t stream);
+hipError_t launch_bwd_dkv2_mfma(const BwdParams& p, hipStream_t stream);
+
+}  // namespace sa

@@ -27,33 +27,9 @@
 // kernels (any D in {16..512}, DV in {16..256}); they are not MFMA-tiled.
 #include "sa_generic.h"
 #include "sa_launch.h"
+#include "sa_backward.h"
 
 namespace sa {
-
-struct BwdParams {
-  const void* q;
-  const void* k1;
-  const void* k2;
-  const void* v1;
-  const void* v2;
-  const void* out;
-  const float* lse;
-  const void* dout;
-  void* dq;
-  void* dk1;
-  void* dk2;
-  void* dv1;
-  void* dv2;
-  float* delta;  // [tokens, hq] workspace: dout·out - dlse
-  float* dl;     // [tokens, hq] workspace: dlse (0 without an LSE gradient)
-  const float* dlse;  // optional gradient of the LSE output
-  int64_t dlse_st;
-  const int32_t* cu;
-  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, lse_st;
-  int64_t do_st, do_sh, dq_st, dq_sh, dk_st, dk_sh, dv_st, dv_sh;
-  int tokens, seqlen, num_seqs, hq, hk, group, ws, wl, d, dv;
-  float scale;
-};
 
 constexpr int kBwdThreads = 256;
 constexpr int kBwdJB = 16;  // rows per group
@@ -553,10 +529,25 @@ static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
     e = hipFuncSetAttribute(k.f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)k.lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(bwd_dq_kernel<T>, ks[0].grid, dim3(kBwdThreads), ks[0].lds, stream, p);
-  hipLaunchKernelGGL(bwd_dkv1_kernel<T>, ks[1].grid, dim3(kBwdThreads), ks[1].lds, stream, p);
-  hipLaunchKernelGGL(bwd_dkv2_kernel<T>, ks[2].grid, dim3(kBwdThreads), ks[2].lds, stream, p);
-  return hipGetLastError();
+  // each pass runs on MFMA tiles where its kernel covers the call, else on the portable kernel
+  e = launch_bwd_dq_mfma(p, stream);
+  if (e == hipErrorNotSupported) {
+    hipLaunchKernelGGL(bwd_dq_kernel<T>, ks[0].grid, dim3(kBwdThreads), ks[0].lds, stream, p);
+    e = hipGetLastError();
+  }
+  if (e != hipSuccess) return e;
+  e = launch_bwd_dkv1_mfma(p, stream);
+  if (e == hipErrorNotSupported) {
+    hipLaunchKernelGGL(bwd_dkv1_kernel<T>, ks[1].grid, dim3(kBwdThreads), ks[1].lds, stream, p);
+    e = hipGetLastError();
+  }
+  if (e != hipSuccess) return e;
+  e = launch_bwd_dkv2_mfma(p, stream);
+  if (e == hipErrorNotSupported) {
+    hipLaunchKernelGGL(bwd_dkv2_kernel<T>, ks[2].grid, dim3(kBwdThreads), ks[2].lds, stream, p);
+    e = hipGetLastError();
+  }
+  return e;
 }
 
 hipError_t launch_prefill_bwd(const sa_prefill_bwd_args* a, void* ws, hipStream_t stream) {
@@ -609,6 +600,7 @@ hipError_t launch_prefill_bwd(const sa_prefill_bwd_args* a, void* ws, hipStream_
   p.d = f.head_dim;
   p.dv = f.value_dim;
   p.scale = f.scale;
+  p.mfma = f.dtype == SA_DTYPE_BF16 && !(f.flags & SA_FLAG_FORCE_GENERIC);
   if (f.dtype == SA_DTYPE_F32) return launch_bwd_t<float>(p, stream);
   return launch_bwd_t<bf16>(p, stream);
 }

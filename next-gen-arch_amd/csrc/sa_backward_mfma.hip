@@ -1,0 +1,369 @@
+// MFMA backward passes of the 2-simplicial prefill (bf16, score width ==
+// value width D in {64, 128}).  Same mathematics, rounding points and
+// atomics-free three-pass split as the portable kernels of sa_backward.hip
+// (archlab/architectures/simplicial_kernels.py:55-106), on 32x32x16 bf16 MFMA
+// tiles:
+//
+// Per query t, head h, short key j, long key k (a_j = bf16(q ⊙ k1_j),
+// b_j = bf16(dout ⊙ v1_j), P = exp(scale a_j·k2_k - lse_t)):
+//   dq pass   (one wave per (t, h), 32 rows j; K2/V2 tiles stream through LDS)
+//     S^T  = K2 · A^T,  dP^T = V2 · B^T          (keys x j)
+//     dS   = bf16(P (dP - delta_t) scale)
+//     dA^T += K2^T · dS^T                        (d x j; transposing K reads)
+//     dq_t = Σ_j dA_j ⊙ k1_j
+//
+// The tile machinery (LDS ring filled by global->LDS DMA, TileGeom layouts,
+// the transposing-read accumulation) is the forward kernel's (sa_mfma.h).
+#include "sa_mfma.h"
+#include "sa_launch.h"
+#include "sa_backward.h"
+
+namespace sa {
+
+namespace {
+
+// Wave-level tile products used by the backward passes (D = head dim).
+template <int D>
+struct BwdOps {
+  using RB = RowBlock<D, D>;
+
+  // C = Tile · X^T over D: A operand = tile rows row0 .. row0+31 (row stride
+  // RS bytes), B operand = the fragments x[D/16] (one 32-row block, k = d).
+  // Lane (n, half) receives C[tile row 8*(r/4) + 4*half + r%4][x row n].
+  template <int RS>
+  __device__ static __forceinline__ floatx16 rows_x(const char* tile, int row0, int lane, const bf16x8* x) {
+    const int n = lane & 31, half = lane >> 5;
+    const char* kp = tile + (row0 + n) * RS + 16 * half;
+    floatx16 c = floatx16{};
+    // fragments are read one step ahead of their MFMA; the scheduling barriers
+    // keep the compiler from hoisting all D/16 reads (D/4 more live VGPRs)
+    bf16x8 f = *(const bf16x8*)kp;
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) {
+      bf16x8 fn;
+      if (t + 1 < D / 16) fn = *(const bf16x8*)(kp + 32 * (t + 1));
+      __builtin_amdgcn_sched_barrier(0);
+      c = mfma32x32x16(f, x[t], c);
+      __builtin_amdgcn_sched_barrier(0);
+      f = fn;
+    }
+    return c;
+  }
+
+  // acc[db] += Tile^T · PB: A operand = the tile's rows row0 .. row0+31
+  // transposed (d x rows, read with ds_read_b64_tr_b16), B operand = {pb0,
+  // pb1}: the 32 x 32 values of a rows_x result (rows x columns) packed by
+  // pack_c.  acc[db] holds d = 32*db + acc_row(r, half), column lane % 32.
+  template <int RS>
+  __device__ static __forceinline__ void tr_acc(floatx16* acc, const char* tile, int row0, int lane,
+                                                const bf16x8& pb0, const bf16x8& pb1) {
+    const int half = lane >> 5, g16 = (lane >> 4) & 1, i16 = lane & 15;
+    const int e_src = i16 >> 2, q_src = i16 & 3;
+    const uint32_t vp = lds_addr(tile + (row0 + 4 * half + e_src) * RS + 32 * g16 + 8 * q_src);
+    constexpr int kSteps = 2 * (D / 32);
+    shortx4 v1, v2;
+    RB::template vread<RS, 0>(vp, v1, v2);
+    lds_wait(v1, v2);
+    static_for<0, kSteps>([&](auto st) {
+      constexpr int step = decltype(st)::value;
+      shortx8 vv = {v1[0], v1[1], v1[2], v1[3], v2[0], v2[1], v2[2], v2[3]};
+      const bf16x8 vf = __builtin_bit_cast(bf16x8, vv);
+      shortx4 n1, n2;
+      if constexpr (step + 1 < kSteps) RB::template vread<RS, step + 1>(vp, n1, n2);
+      __builtin_amdgcn_sched_barrier(0);
+      acc[step % (D / 32)] = mfma32x32x16(vf, step / (D / 32) == 0 ? pb0 : pb1, acc[step % (D / 32)]);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (step + 1 < kSteps) {
+        lds_wait(n1, n2);
+        v1 = n1;
+        v2 = n2;
+      }
+    });
+  }
+
+  // 16 C-layout values (rows x this lane's column) -> the B operand of tr_acc
+  // (bf16, round to nearest even).
+  __device__ static __forceinline__ void pack_c(const float* x, bf16x8& pb0, bf16x8& pb1) {
+    uint32_t pk[8];
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) pk[r >> 1] = pack_bf16(x[r], x[r + 1]);
+    pb0 = __builtin_bit_cast(bf16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
+    pb1 = __builtin_bit_cast(bf16x8, u32x4{pk[4], pk[5], pk[6], pk[7]});
+  }
+};
+
+struct BwdGeo {
+  int nc;       // long-axis chunks per query: ceil(wl / 32)
+  int nr;       // short-axis row groups: ceil(ws / 32)
+  int qblocks;  // query blocks per head group
+  int hsub;     // head sub-groups per KV group
+  int nblocks;
+};
+
+// ---------------------------------------------------------------------------
+// dq: a workgroup of 4 waves owns NQ consecutive queries x NH heads of one KV
+// group (the forward kernel's blocking); chunk c of the NQ queries' long
+// windows is one K2/V2 tile of 32 + NQ - 1 rows.
+template <int D, int NQ, int NH, int P>
+__global__ __launch_bounds__(64 * NQ * NH, 2) void bwd_dq_mfma_kernel(BwdParams p, BwdGeo geo) {
+  static_assert(NQ * NH == 4, "4 waves per block");
+  constexpr int NW = NQ * NH;
+  constexpr int ROWS = kChunk + NQ - 1;
+  using G = TileGeom<D, D, ROWS, NW>;
+  using OPS = BwdOps<D>;
+  constexpr int R = P + 1;
+  constexpr int NI = G::NI;
+  // ring of R tile slots, also the per-wave reduction scratch of the epilogue
+  constexpr int RING = R * G::SLOT > NW * 64 * 36 * 4 ? R * G::SLOT : NW * 64 * 36 * 4;
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  char* const sslot = lds + RING;         // k1 rows (K region), v1 rows (V region) of the pass
+  char* const qslot = sslot + G::SLOT;    // q rows 0..NW-1, dout rows NW..2NW-1 (row stride RSK)
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hw = wid % NH, qo = wid / NH;
+  const int half = lane >> 5, n = lane & 31;
+
+  const int lb = xcd_remap(blockIdx.x, geo.nblocks);
+  const int qb = lb % geo.qblocks;
+  const int hg = lb / geo.qblocks;
+  const int g = hg / geo.hsub, hs = hg % geo.hsub;
+  const int t0 = qb * NQ;
+  if (t0 >= p.tokens) return;
+
+  const int t = __builtin_amdgcn_readfirstlane(t0 + qo);
+  const bool qvalid = t < p.tokens;
+  const int h = __builtin_amdgcn_readfirstlane(g * p.group + hs * NH + hw);
+  const int s0 = qvalid ? seq_start(p.cu, p.num_seqs, p.seqlen, t) : 0;
+  const int lo2 = __builtin_amdgcn_readfirstlane(max(s0, t - p.wl + 1));
+  const int lo1 = __builtin_amdgcn_readfirstlane(max(s0, t - p.ws + 1));
+  const int cfirst = __builtin_amdgcn_readfirstlane(qvalid ? (lo2 - (t - p.wl + 1)) / kChunk : geo.nc);
+  int c0 = geo.nc;  // first step in which any query of the block has a valid key
+#pragma unroll
+  for (int w = 0; w < NQ; ++w) {
+    const int tw = t0 + w;
+    if (tw < p.tokens) {
+      const int sw = seq_start(p.cu, p.num_seqs, p.seqlen, tw);
+      c0 = min(c0, (max(sw, tw - p.wl + 1) - (tw - p.wl + 1)) / kChunk);
+    }
+  }
+  c0 = __builtin_amdgcn_readfirstlane(c0);
+
+  const int kb0 = t0 - p.wl + 1;  // key of tile row 0 at chunk 0
+  const int last = p.tokens - 1;
+  const int64_t k_st = p.k_st, v_st = p.v_st;
+  const int64_t k_g = (int64_t)g * p.k_sh, v_g = (int64_t)g * p.v_sh;
+  const bf16* const k1 = (const bf16*)p.k1;
+  const bf16* const k2 = (const bf16*)p.k2;
+  const bf16* const v1 = (const bf16*)p.v1;
+  const bf16* const v2 = (const bf16*)p.v2;
+
+  uint32_t voff[NI];
+#pragma unroll
+  for (int k = 0; k < NI; ++k) {
+    int is_v, row, seg;
+    G::decode(wid, k, lane, is_v, row, seg);
+    voff[k] = (uint32_t)(((int64_t)row * (is_v ? v_st : k_st) + seg * 8) * 2);
+  }
+  // One tile of rows kb .. kb+ROWS-1: K region from kt, V region from vt.
+  auto dma_tile = [&](char* slot, int kb_in, const bf16* kt, const bf16* vt) {
+    const int kb = __builtin_amdgcn_readfirstlane(kb_in);
+    if (kb >= 0 && kb + ROWS - 1 <= last) {
+      const char* kbase = (const char*)(kt + (int64_t)kb * k_st + k_g);
+      const char* vbase = (const char*)(vt + (int64_t)kb * v_st + v_g);
+#pragma unroll
+      for (int k = 0; k < NI; ++k)
+        dma16(uniform_ptr(G::instr_is_v(wid, k) ? vbase : kbase) + voff[k], G::dst(slot, wid, k));
+    } else {  // the tile crosses the tensor edge: clamp every row into [0, tokens)
+#pragma unroll
+      for (int k = 0; k < NI; ++k) {
+        int is_v, row, seg;
+        G::decode(wid, k, lane, is_v, row, seg);
+        const int64_t key = min(max(kb + row, 0), last);
+        const bf16* src = is_v ? vt + key * v_st + v_g : kt + key * k_st + k_g;
+        dma16(src + seg * 8, G::dst(slot, wid, k));
+      }
+    }
+  };
+  auto issue = [&](int c) { dma_tile(lds + (c % R) * G::SLOT, kb0 + kChunk * c, k2, v2); };
+  // q and dout rows of the NW (query, head) pairs (wave 0; QI instructions)
+  constexpr int QI = (2 * NW * G::RSK + 1023) / 1024;
+  auto dma_qd = [&]() {
+    if (wid == 0) {
+#pragma unroll
+      for (int k = 0; k < QI; ++k) {
+        const int b = k * 1024 + lane * 16;
+        int row = b / G::RSK, seg = (b % G::RSK) >> 4;
+        if (row >= 2 * NW || seg >= G::kSegsK) row = 0, seg = 0;
+        const int pr = row % NW;
+        const int tq = min(t0 + pr / NH, last);
+        const int hq = g * p.group + hs * NH + pr % NH;
+        const bf16* src = row < NW ? (const bf16*)p.q + (int64_t)tq * p.q_st + (int64_t)hq * p.q_sh
+                                   : (const bf16*)p.dout + (int64_t)tq * p.do_st + (int64_t)hq * p.do_sh;
+        dma16(src + seg * 8, qslot + k * 1024);
+      }
+    }
+  };
+
+  const int64_t th = (int64_t)min(t, last) * p.hq + h;
+  const float lse2 = qvalid ? p.lse[(int64_t)min(t, last) * p.lse_st + h] * kLog2e : 0.f;
+  const float delta = qvalid ? p.delta[th] : 0.f;
+  const float dl = qvalid ? p.dl[th] : 0.f;
+  const bool single = t == s0 || (p.ws == 1 && p.wl == 1);  // one valid pair: only the LSE-gradient term
+  const float sl2s = p.scale * kLog2e;
+  // dS = P (dP - delta) scale, or P dlse scale for a single pair: P (dP dpm + dsm)
+  const float dpm = single ? 0.f : p.scale;
+  const float dsm = single ? dl * p.scale : -delta * p.scale;
+
+  RowBlock<D, D> ra, rbv;  // A rows (q ⊙ k1) and B rows (dout ⊙ v1); only their fragments are used
+  float dqrun[D / 64];
+#pragma unroll
+  for (int i = 0; i < D / 64; ++i) dqrun[i] = 0.f;
+
+  for (int r = 0; r < geo.nr; ++r) {
+    const int j = t - 32 * r - n;  // this lane's short-axis key
+    const bool row_ok = qvalid && j >= lo1;
+    const int kbs = t0 - 31 - 32 * r;  // short-slot row 0
+    dma_tile(sslot, kbs, k1, v1);
+    if (r == 0) dma_qd();
+#pragma unroll
+    for (int e = 0; e < P; ++e) issue(c0 + e);  // unconditional: static count for the wait below
+    wait_vmcnt<P * NI>();
+    block_barrier();
+    const int srow = qo + 31 - n;  // row of key j in the short slot
+    ra.form_a_lds(sslot + srow * G::RSK, qslot + wid * G::RSK, row_ok, half, false);
+    rbv.form_a_lds(sslot + G::VOFF + srow * G::RSV, qslot + (NW + wid) * G::RSK, row_ok, half, false);
+
+    floatx16 dA[D / 32];
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) dA[i] = floatx16{};
+    for (int c = c0; c < geo.nc; ++c) {
+      wait_tiles<NI, P>(min(P - 1, geo.nc - 1 - c));
+      block_barrier();  // tile c complete for every wave; the slot of tile c-1 is free
+      if (c + P < geo.nc) issue(c + P);
+      const bool active = qvalid && c >= cfirst;
+      const int kfirst = t - p.wl + 1 + kChunk * c;  // key of this wave's chunk row 0
+      const int klo = active ? max(lo2 - kfirst, 0) : kChunk;
+      const int khi = active ? min(t - kfirst, kChunk - 1) : -1;
+      const char* slot = lds + (c % R) * G::SLOT;
+      const floatx16 s = OPS::template rows_x<G::RSK>(slot, qo, lane, ra.a);
+      const floatx16 dp = OPS::template rows_x<G::RSV>(slot + G::VOFF, qo, lane, rbv.a);
+      // register r holds chunk key 8*(r/4) + r%4 + 4*half of column j = this lane's row
+      const int lo_h = klo - 4 * half, hi_h = khi - 4 * half;
+      float ds[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int kr = 8 * (e >> 2) + (e & 3);
+        const bool ok = row_ok && kr >= lo_h && kr <= hi_h;
+        const float pr = ok ? fast_exp2(fmaf(s[e], sl2s, -lse2)) : 0.f;
+        ds[e] = pr * fmaf(dp[e], dpm, dsm);
+      }
+      bf16x8 pb0, pb1;
+      OPS::pack_c(ds, pb0, pb1);
+      OPS::template tr_acc<G::RSK>(dA, slot, qo, lane, pb0, pb1);  // dA^T += K2^T · dS^T
+    }
+    wait_vmcnt<0>();
+    block_barrier();  // ring reads done (LDS reused below)
+
+    // dq[d] += Σ_j dA_j[d] k1_j[d] over the wave's 32 rows
+    float* red = (float*)lds + wid * (64 * 36);  // [64 d][36] per wave (ring region)
+    const char* k1s = sslot + srow * G::RSK;     // this lane's k1 row
+    bf16x4 kv[D / 64][2][4];
+#pragma unroll
+    for (int sl = 0; sl < D / 64; ++sl)
+#pragma unroll
+      for (int dbl = 0; dbl < 2; ++dbl)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4)
+          kv[sl][dbl][q4] = *(const bf16x4*)(k1s + 2 * (64 * sl + 32 * dbl + 8 * q4 + 4 * half));
+#pragma unroll
+    for (int sl = 0; sl < D / 64; ++sl) {
+#pragma unroll
+      for (int dbl = 0; dbl < 2; ++dbl) {
+        const int db = 2 * sl + dbl;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int dd = 32 * dbl + 8 * q4 + 4 * half;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float k = row_ok ? (float)kv[sl][dbl][q4][e] : 0.f;
+            red[(dd + e) * 36 + n] = k * dA[db][4 * q4 + e];
+          }
+        }
+      }
+      // `red` is private to this wave and a wave's LDS accesses execute in order
+      float acc = 0.f;
+      const floatx4* row4 = (const floatx4*)(red + lane * 36);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        floatx4 x = row4[i];
+        acc += (x[0] + x[1]) + (x[2] + x[3]);
+      }
+      dqrun[sl] += acc;
+    }
+    block_barrier();  // every wave's `red` reads done before the next pass (or exit) reuses the LDS
+  }
+
+  if (qvalid) {
+    bf16* orow = (bf16*)p.dq + (int64_t)t * p.dq_st + (int64_t)h * p.dq_sh;
+#pragma unroll
+    for (int i = 0; i < D / 64; ++i) orow[64 * i + lane] = (bf16)dqrun[i];
+  }
+}
+
+template <int D, int NQ, int NH>
+hipError_t launch_dq_t(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
+  constexpr int P = 1;  // one tile in flight: ring + short slot + q/dout rows stay <= 80 KB (2 per CU)
+  geo.qblocks = (p.tokens + NQ - 1) / NQ;
+  geo.hsub = p.group / NH;
+  geo.nblocks = geo.qblocks * p.hk * geo.hsub;
+  constexpr int NW = NQ * NH;
+  using G = TileGeom<D, D, kChunk + NQ - 1, NW>;
+  const size_t qslot = ((size_t)2 * NW * G::RSK + 1023) / 1024 * 1024;
+  const size_t ring = (size_t)(P + 1) * G::SLOT, red = (size_t)NW * 64 * 36 * sizeof(float);
+  const size_t lds = (ring > red ? ring : red) + G::SLOT + qslot;
+  auto kern = bwd_dq_mfma_kernel<D, NQ, NH, P>;
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(geo.nblocks), dim3(64 * NW), lds, stream, p, geo);
+  return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_dq_d(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
+  if (p.group % 4 == 0) return launch_dq_t<D, 1, 4>(p, geo, stream);
+  if (p.group % 2 == 0) return launch_dq_t<D, 2, 2>(p, geo, stream);
+  return launch_dq_t<D, 4, 1>(p, geo, stream);
+}
+
+// bf16, DK == DV in {64, 128}, 16-byte aligned rows.
+bool bwd_mfma_ok(const BwdParams& p) {
+  if (!p.mfma) return false;
+  if (p.d != p.dv || (p.d != 64 && p.d != 128)) return false;
+  const int64_t st[] = {p.q_st, p.q_sh, p.k_st, p.k_sh, p.v_st, p.v_sh, p.do_st, p.do_sh};
+  for (int64_t s : st)
+    if (s % 8) return false;
+  const uintptr_t ptrs = (uintptr_t)p.q | (uintptr_t)p.k1 | (uintptr_t)p.k2 | (uintptr_t)p.v1 |
+                         (uintptr_t)p.v2 | (uintptr_t)p.dout;
+  return (ptrs & 15) == 0;
+}
+
+BwdGeo base_geo(const BwdParams& p) {
+  BwdGeo geo{};
+  geo.nc = (p.wl + kChunk - 1) / kChunk;
+  geo.nr = (p.ws + 31) / 32;
+  return geo;
+}
+
+}  // namespace
+
+hipError_t launch_bwd_dq_mfma(const BwdParams& p, hipStream_t stream) {
+  if (!bwd_mfma_ok(p)) return hipErrorNotSupported;
+  const BwdGeo geo = base_geo(p);
+  return p.d == 64 ? launch_dq_d<64>(p, geo, stream) : launch_dq_d<128>(p, geo, stream);
+}
+
+hipError_t launch_bwd_dkv1_mfma(const BwdParams&, hipStream_t) { return hipErrorNotSupported; }
+hipError_t launch_bwd_dkv2_mfma(const BwdParams&, hipStream_t) { return hipErrorNotSupported; }
+
+}  // namespace sa

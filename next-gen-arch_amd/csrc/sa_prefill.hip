@@ -51,29 +51,6 @@ struct PrefillParams {
   int nblocks;    // total blocks
 };
 
-// Start of token t's sequence, clamped to [0, t] so that a malformed
-// cu_seqlens cannot move any row access outside the tensors.
-__device__ __forceinline__ int seq_start(const int32_t* cu, int num_seqs, int seqlen, int t) {
-  if (cu == nullptr) return (t / seqlen) * seqlen;
-  int lo = 0, hi = num_seqs - 1;  // largest s with cu[s] <= t
-  while (lo < hi) {
-    int mid = (lo + hi + 1) >> 1;
-    if (cu[mid] <= t) lo = mid;
-    else hi = mid - 1;
-  }
-  // uniform across the wave (every lane searched the same t): keep it scalar
-  return __builtin_amdgcn_readfirstlane(min(max(cu[lo], 0), t));
-}
-
-// Workgroups are dispatched round-robin over the 8 XCDs; remap so that each
-// XCD (own L2) walks a contiguous range of logical blocks (neighbouring
-// queries of the same heads share their key windows).
-__device__ __forceinline__ int xcd_remap(int b, int n) {
-  const int q = n / 8, r = n % 8;
-  const int x = b % 8, i = b / 8;
-  return x * q + min(x, r) + i;
-}
-
 #ifndef SA_PREFILL_WAVES_PER_SIMD
 #define SA_PREFILL_WAVES_PER_SIMD 2
 #endif

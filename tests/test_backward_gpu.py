@@ -112,3 +112,52 @@ def test_backward_varlen_equals_per_sequence(cuda):
         for a, b in zip(xd, xs):
             torch.testing.assert_close(a.grad[start:start + n], b.grad[0], rtol=0, atol=0)
         start += n
+
+
+# ---- the MFMA passes (bf16, D == DV in {64, 128}) ------------------------------
+
+@pytest.mark.parametrize("hq,hk,d,ws,wl", [(4, 4, 128, 40, 130), (8, 2, 64, 32, 512), (4, 1, 128, 7, 33),
+                                           (2, 2, 128, 1, 1)])
+def test_backward_bf16_mfma_shapes(cuda, hq, hk, d, ws, wl):
+    """Two short passes (ws 40), a long window wider than the sequence, GQA 4, single pairs."""
+    _run(cuda, 1, 200, hq, hk, d, ws, wl, torch.bfloat16, seed=hq + ws)
+
+
+def test_backward_bf16_negative_scale(cuda):
+    _run(cuda, 1, 60, 4, 2, 128, 8, 40, torch.bfloat16, scale=-0.08)
+
+
+def test_backward_bf16_varlen_with_lse_gradient(cuda):
+    """Packed sequences (every sequence start is a single-pair query) and a gradient on the LSE."""
+    from archlab_amd import simplicial_varlen_attention
+    lengths = [1, 45, 3, 80]
+    t = sum(lengths)
+    x = [v[0] for v in rand_inputs(1, t, 8, 2, 128, seed=21, dtype=torch.bfloat16)]
+    g = torch.Generator().manual_seed(5)
+    dout = torch.randn(t, 8, 128, generator=g).bfloat16()
+    dl = torch.randn(t, 8, generator=g)
+    cu = torch.tensor([0, 1, 46, 49, 129], dtype=torch.int32)
+    xd = [v.to(cuda).requires_grad_(True) for v in x]
+    out, lse = simplicial_varlen_attention(*xd, cu.to(cuda), 12, 50, return_lse=True)
+    ((out.float() * dout.to(cuda).float()).sum() + (lse * dl.to(cuda)).sum()).backward()
+    xs = [v.double().requires_grad_(True) for v in x]
+    o, l = O.varlen_reference(*xs, cu, 12, 50, scale=128 ** -0.5, return_lse=True)
+    ((o * dout.double()).sum() + (l * dl.double()).sum()).backward()
+    _assert_grads([v.grad for v in xd], [v.grad.float() for v in xs], torch.bfloat16, "varlen bf16 + dlse")
+
+
+def test_backward_mfma_matches_portable(cuda):
+    """The MFMA passes and the portable kernels agree to bf16 precision on the same inputs."""
+    from archlab_amd import simplicial_attention
+    x = [t.to(cuda) for t in rand_inputs(1, 150, 8, 2, 128, seed=12, dtype=torch.bfloat16)]
+    dout = torch.randn(1, 150, 8, 128, device=cuda).bfloat16()
+    grads = {}
+    for kernel in ("auto", "generic"):
+        xd = [t.clone().requires_grad_(True) for t in x]
+        simplicial_attention(*xd, 32, 96, kernel=kernel).backward(dout)
+        grads[kernel] = [t.grad.float() for t in xd]
+    for name, a, b in zip(("dq", "dk1", "dk2", "dv1", "dv2"), grads["auto"], grads["generic"]):
+        err = (a - b).abs().max().item()
+        bound = 2e-2 * max(b.abs().max().item(), 1.0)
+        print(f"mfma vs portable {name}: {err:.2e} / {bound:.1e}", flush=True)
+        assert err <= bound, name
