@@ -11,6 +11,12 @@
 //     dS   = bf16(P (dP - delta_t) scale)
 //     dA^T += K2^T · dS^T                        (d x j; transposing K reads)
 //     dq_t = Σ_j dA_j ⊙ k1_j
+//   dk1/dv1 pass (one wave per (j, h); its 32 rows are the queries
+//   t = j + 32r + n whose short window holds j; tiles span the rows' union of
+//   long windows, masked per row)
+//     S^T, dP^T, dS as above (A rows q_t ⊙ k1_j, B rows dout_t ⊙ v1_j)
+//     G^T  += K2^T · dS^T,  O''^T += V2^T · bf16(P)^T     (d x t)
+//     dk1_j = Σ_h Σ_t G_t ⊙ q_t,   dv1_j = Σ_h Σ_t O''_t ⊙ dout_t
 //
 // The tile machinery (LDS ring filled by global->LDS DMA, TileGeom layouts,
 // the transposing-read accumulation) is the forward kernel's (sa_mfma.h).
@@ -336,6 +342,287 @@ hipError_t launch_dq_d(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
   return launch_dq_t<D, 4, 1>(p, geo, stream);
 }
 
+
+// ---------------------------------------------------------------------------
+// dk1, dv1: a workgroup of 4 waves owns 4 consecutive short keys of one KV
+// group and loops over the group's query heads, so that every (j, KV group)
+// is summed over all its heads inside one workgroup.  Wave (j = j0 + wave,
+// head h) has rows t = j + 32r + n (pass r); chunk c of its rows' long windows
+// covers keys j + 32r - wl + 1 + 32c + [0, 32).  The 4 waves share one K2/V2
+// tile of 35 rows per chunk and one slot of q / dout rows (head h, queries
+// j0 + 32r .. +34).
+// Two accumulator sets (G, O'') and both fragment sets need one wave per SIMD
+// at D = 128.
+template <int D, int NQ, int NH, int P>
+__global__ __launch_bounds__(64 * NQ * NH, (D >= 128 ? 1 : 2)) void bwd_dkv1_mfma_kernel(BwdParams p, BwdGeo geo) {
+  static_assert(NQ == 4 && NH == 1, "4 keys per block, one head at a time");
+  constexpr int NW = NQ * NH;
+  constexpr int ROWS = kChunk + NQ - 1;
+  using G = TileGeom<D, D, ROWS, NW>;
+  using OPS = BwdOps<D>;
+  constexpr int R = P + 1;
+  constexpr int NI = G::NI;
+  constexpr int RING = R * G::SLOT > NW * 64 * 36 * 4 ? R * G::SLOT : NW * 64 * 36 * 4;
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  char* const rslot = lds + RING;       // q rows (K region) and dout rows (V region) of the pass's queries
+  char* const kslot = rslot + G::SLOT;  // k1 rows 0..NW-1, v1 rows NW..2NW-1 (row stride RSK)
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hw = wid % NH, qo = wid / NH;
+  const int half = lane >> 5, n = lane & 31;
+
+  const int lb = xcd_remap(blockIdx.x, geo.nblocks);
+  const int jb = lb % geo.qblocks;
+  const int g = lb / geo.qblocks;
+  const int j0 = jb * NQ;
+  if (j0 >= p.tokens) return;
+  const int last = p.tokens - 1;
+  const int j = __builtin_amdgcn_readfirstlane(j0 + qo);
+  const bool jvalid = j < p.tokens;
+  const int jc = min(j, last);
+  // the sequence of key j: rows t in [j, send) share it
+  const int s0 = seq_start(p.cu, p.num_seqs, p.seqlen, jc);
+  int send;
+  if (p.cu == nullptr) {
+    send = s0 + p.seqlen;
+  } else {
+    int lo = 0, hi = p.num_seqs - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (p.cu[mid] <= jc) lo = mid;
+      else hi = mid - 1;
+    }
+    send = min(p.cu[lo + 1], p.tokens);
+  }
+  send = __builtin_amdgcn_readfirstlane(max(send, jc + 1));
+
+  const int64_t k_st = p.k_st, v_st = p.v_st;
+  const int64_t k_g = (int64_t)g * p.k_sh, v_g = (int64_t)g * p.v_sh;
+  const bf16* const k2 = (const bf16*)p.k2;
+  const bf16* const v2 = (const bf16*)p.v2;
+
+  uint32_t koff[NI];  // this lane's byte offsets in a K2/V2 tile
+#pragma unroll
+  for (int k = 0; k < NI; ++k) {
+    int is_v, row, seg;
+    G::decode(wid, k, lane, is_v, row, seg);
+    koff[k] = (uint32_t)(((int64_t)row * (is_v ? v_st : k_st) + seg * 8) * 2);
+  }
+  // One tile of rows kb .. kb+ROWS-1 of (kt: K region, vt: V region), rows
+  // clamped into [0, tokens) at the tensor edges.
+  auto dma_rows = [&](char* slot, int kb_in, const bf16* kt, int64_t kst, int64_t kof, const bf16* vt, int64_t vst,
+                      int64_t vof, const uint32_t* off) {
+    const int kb = __builtin_amdgcn_readfirstlane(kb_in);
+    if (kb >= 0 && kb + ROWS - 1 <= last) {
+      const char* kbase = (const char*)(kt + (int64_t)kb * kst + kof);
+      const char* vbase = (const char*)(vt + (int64_t)kb * vst + vof);
+#pragma unroll
+      for (int k = 0; k < NI; ++k)
+        dma16(uniform_ptr(G::instr_is_v(wid, k) ? vbase : kbase) + off[k], G::dst(slot, wid, k));
+    } else {
+#pragma unroll
+      for (int k = 0; k < NI; ++k) {
+        int is_v, row, seg;
+        G::decode(wid, k, lane, is_v, row, seg);
+        const int64_t key = min(max(kb + row, 0), last);
+        const bf16* src = is_v ? vt + key * vst + vof : kt + key * kst + kof;
+        dma16(src + seg * 8, G::dst(slot, wid, k));
+      }
+    }
+  };
+  // k1 and v1 rows of the NW waves' keys (wave 0)
+  constexpr int KI = (2 * NW * G::RSK + 1023) / 1024;
+  auto dma_kv = [&]() {
+    if (wid == 0) {
+#pragma unroll
+      for (int k = 0; k < KI; ++k) {
+        const int b = k * 1024 + lane * 16;
+        int row = b / G::RSK, seg = (b % G::RSK) >> 4;
+        if (row >= 2 * NW || seg >= G::kSegsK) row = 0, seg = 0;
+        const int jr = min(j0 + (row % NW) / NH, last);
+        const bf16* src = row < NW ? (const bf16*)p.k1 + (int64_t)jr * k_st + k_g
+                                   : (const bf16*)p.v1 + (int64_t)jr * v_st + v_g;
+        dma16(src + seg * 8, kslot + k * 1024);
+      }
+    }
+  };
+
+  const float sl2s = p.scale * kLog2e;
+  float dk1run[D / 64], dv1run[D / 64];
+#pragma unroll
+  for (int i = 0; i < D / 64; ++i) dk1run[i] = dv1run[i] = 0.f;
+  RowBlock<D, D> ra, rbv;  // A rows (q_t ⊙ k1_j), B rows (dout_t ⊙ v1_j)
+  const int nc = (p.wl + 2 * kChunk - 2) / kChunk;  // chunks over wl + 31 keys
+  dma_kv();
+  bool first = true;
+
+  for (int hs = 0; hs < geo.hsub; ++hs) {
+    const int h = __builtin_amdgcn_readfirstlane(g * p.group + hs * NH + hw);
+    // q / dout rows of head h: the row slot uses the q and dout strides
+    uint32_t roff[NI];
+#pragma unroll
+    for (int k = 0; k < NI; ++k) {
+      int is_v, row, seg;
+      G::decode(wid, k, lane, is_v, row, seg);
+      roff[k] = (uint32_t)(((int64_t)row * (is_v ? p.do_st : p.q_st) + seg * 8) * 2);
+    }
+    for (int r = 0; r < geo.nr; ++r) {
+      const int t = j + 32 * r + n;  // this lane's row (query)
+      const bool row_ok = jvalid && 32 * r + n < p.ws && t < send;
+      const int tc = min(t, last);
+      const int64_t th = (int64_t)tc * p.hq + h;
+      const float lse2 = row_ok ? p.lse[(int64_t)tc * p.lse_st + h] * kLog2e : 0.f;
+      const bool single = t == s0 || (p.ws == 1 && p.wl == 1);
+      const float dpm = single ? 0.f : p.scale;
+      const float dsm = row_ok ? (single ? p.dl[th] * p.scale : -p.delta[th] * p.scale) : 0.f;
+      const int kb0 = j0 + 32 * r - p.wl + 1;  // key of tile row 0 at chunk 0
+      const int tb0 = j0 + 32 * r;             // query of row-slot row 0
+      if (!first) block_barrier();  // the previous pass's epilogue reads of the LDS are done
+      first = false;
+      dma_rows(rslot, tb0, (const bf16*)p.q, p.q_st, (int64_t)h * p.q_sh, (const bf16*)p.dout, p.do_st,
+               (int64_t)h * p.do_sh, roff);
+      auto issue = [&](int c) {
+        dma_rows(lds + (c % R) * G::SLOT, kb0 + kChunk * c, k2, k_st, k_g, v2, v_st, v_g, koff);
+      };
+#pragma unroll
+      for (int e = 0; e < P; ++e) issue(e);
+      wait_vmcnt<P * NI>();
+      block_barrier();
+      const int srow = qo + n;  // row of query t in the row slot
+      // kslot row w holds the k1 (v1: row NW + w) row of key j0 + w / NH, i.e. this wave's key
+      ra.form_a_lds(rslot + srow * G::RSK, kslot + wid * G::RSK, row_ok, half, false);
+      rbv.form_a_lds(rslot + G::VOFF + srow * G::RSV, kslot + (NW + wid) * G::RSK, row_ok, half, false);
+
+      floatx16 gacc[D / 32], oacc[D / 32];
+#pragma unroll
+      for (int i = 0; i < D / 32; ++i) gacc[i] = oacc[i] = floatx16{};
+      for (int c = 0; c < nc; ++c) {
+        wait_tiles<NI, P>(min(P - 1, nc - 1 - c));
+        block_barrier();
+        if (c + P < nc) issue(c + P);
+        const int kfirst = j + 32 * r - p.wl + 1 + kChunk * c;  // key of this wave's chunk row 0
+        // per-row key range: max(s0, t - wl + 1) <= k <= t
+        const int klo = max(max(s0 - kfirst, n - kChunk * c), 0);
+        const int khi = min(n + p.wl - 1 - kChunk * c, kChunk - 1);
+        const char* slot = lds + (c % R) * G::SLOT;
+        const floatx16 sv = OPS::template rows_x<G::RSK>(slot, qo, lane, ra.a);
+        const floatx16 dp = OPS::template rows_x<G::RSV>(slot + G::VOFF, qo, lane, rbv.a);
+        const int lo_h = klo - 4 * half, hi_h = khi - 4 * half;
+        // interior chunk: every key valid for every row of the wave (uniform test)
+        const bool interior = s0 <= kfirst && c >= 1 && kChunk * c <= p.wl - kChunk;
+        // P and dS straight into packed bf16 pairs (B operands of the two accumulations)
+        uint32_t pp[8], pd[8];
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+          const int kr0 = 8 * (e >> 2) + (e & 3), kr1 = kr0 + 1;
+          const bool ok0 = row_ok && (interior || (kr0 >= lo_h && kr0 <= hi_h));
+          const bool ok1 = row_ok && (interior || (kr1 >= lo_h && kr1 <= hi_h));
+          const float p0 = ok0 ? fast_exp2(fmaf(sv[e], sl2s, -lse2)) : 0.f;
+          const float p1 = ok1 ? fast_exp2(fmaf(sv[e + 1], sl2s, -lse2)) : 0.f;
+          pp[e >> 1] = pack_bf16(p0, p1);
+          pd[e >> 1] = pack_bf16(p0 * fmaf(dp[e], dpm, dsm), p1 * fmaf(dp[e + 1], dpm, dsm));
+        }
+        const bf16x8 db0 = __builtin_bit_cast(bf16x8, u32x4{pd[0], pd[1], pd[2], pd[3]});
+        const bf16x8 db1 = __builtin_bit_cast(bf16x8, u32x4{pd[4], pd[5], pd[6], pd[7]});
+        OPS::template tr_acc<G::RSK>(gacc, slot, qo, lane, db0, db1);  // G^T += K2^T · dS^T
+        const bf16x8 pb0 = __builtin_bit_cast(bf16x8, u32x4{pp[0], pp[1], pp[2], pp[3]});
+        const bf16x8 pb1 = __builtin_bit_cast(bf16x8, u32x4{pp[4], pp[5], pp[6], pp[7]});
+        OPS::template tr_acc<G::RSV>(oacc, slot + G::VOFF, qo, lane, pb0, pb1);  // O''^T += V2^T · P^T
+      }
+      wait_vmcnt<0>();
+      block_barrier();  // ring reads done (LDS reused below)
+
+      // dk1[d] += Σ_t G_t[d] q_t[d], dv1[d] += Σ_t O''_t[d] dout_t[d] over the wave's rows
+      float* red = (float*)lds + wid * (64 * 36);
+#pragma unroll
+      for (int which = 0; which < 2; ++which) {
+        const char* xs = which == 0 ? rslot + srow * G::RSK : rslot + G::VOFF + srow * G::RSV;
+        bf16x4 xv[D / 64][2][4];
+#pragma unroll
+        for (int sl = 0; sl < D / 64; ++sl)
+#pragma unroll
+          for (int dbl = 0; dbl < 2; ++dbl)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4)
+              xv[sl][dbl][q4] = *(const bf16x4*)(xs + 2 * (64 * sl + 32 * dbl + 8 * q4 + 4 * half));
+#pragma unroll
+        for (int sl = 0; sl < D / 64; ++sl) {
+#pragma unroll
+          for (int dbl = 0; dbl < 2; ++dbl) {
+            const int db = 2 * sl + dbl;
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+              const int dd = 32 * dbl + 8 * q4 + 4 * half;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const float x = row_ok ? (float)xv[sl][dbl][q4][e] : 0.f;
+                red[(dd + e) * 36 + n] = x * (which == 0 ? gacc[db][4 * q4 + e] : oacc[db][4 * q4 + e]);
+              }
+            }
+          }
+          float acc = 0.f;
+          const floatx4* row4 = (const floatx4*)(red + lane * 36);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            floatx4 x = row4[i];
+            acc += (x[0] + x[1]) + (x[2] + x[3]);
+          }
+          if (which == 0) dk1run[sl] += acc;
+          else dv1run[sl] += acc;
+        }
+      }
+    }
+  }
+
+  // sum over the NH waves of each key (heads hw), then write
+  block_barrier();
+  float* sum = (float*)lds;  // [NW][2][D]
+#pragma unroll
+  for (int i = 0; i < D / 64; ++i) {
+    sum[(wid * 2 + 0) * D + 64 * i + lane] = dk1run[i];
+    sum[(wid * 2 + 1) * D + 64 * i + lane] = dv1run[i];
+  }
+  block_barrier();
+  if (hw == 0 && jvalid) {
+    bf16* dk = (bf16*)p.dk1 + (int64_t)j * p.dk_st + (int64_t)g * p.dk_sh;
+    bf16* dv = (bf16*)p.dv1 + (int64_t)j * p.dv_st + (int64_t)g * p.dv_sh;
+#pragma unroll
+    for (int i = 0; i < D / 64; ++i) {
+      float a = 0.f, b = 0.f;
+      for (int w = 0; w < NH; ++w) {
+        a += sum[((wid + w) * 2 + 0) * D + 64 * i + lane];
+        b += sum[((wid + w) * 2 + 1) * D + 64 * i + lane];
+      }
+      dk[64 * i + lane] = (bf16)a;
+      dv[64 * i + lane] = (bf16)b;
+    }
+  }
+}
+
+template <int D, int NQ, int NH>
+hipError_t launch_dkv1_t(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
+  constexpr int P = D >= 128 ? 2 : 1;  // one workgroup per CU at D = 128: LDS for a deeper ring
+  geo.qblocks = (p.tokens + NQ - 1) / NQ;
+  geo.hsub = p.group / NH;
+  geo.nblocks = geo.qblocks * p.hk;
+  constexpr int NW = NQ * NH;
+  using G = TileGeom<D, D, kChunk + NQ - 1, NW>;
+  const size_t kslot = ((size_t)2 * NW * G::RSK + 1023) / 1024 * 1024;
+  const size_t ring = (size_t)(P + 1) * G::SLOT, red = (size_t)NW * 64 * 36 * sizeof(float);
+  const size_t lds = (ring > red ? ring : red) + G::SLOT + kslot;
+  auto kern = bwd_dkv1_mfma_kernel<D, NQ, NH, P>;
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(geo.nblocks), dim3(64 * NW), lds, stream, p, geo);
+  return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_dkv1_d(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
+  return launch_dkv1_t<D, 4, 1>(p, geo, stream);
+}
+
 // bf16, DK == DV in {64, 128}, 16-byte aligned rows.
 bool bwd_mfma_ok(const BwdParams& p) {
   if (!p.mfma) return false;
@@ -363,7 +650,11 @@ hipError_t launch_bwd_dq_mfma(const BwdParams& p, hipStream_t stream) {
   return p.d == 64 ? launch_dq_d<64>(p, geo, stream) : launch_dq_d<128>(p, geo, stream);
 }
 
-hipError_t launch_bwd_dkv1_mfma(const BwdParams&, hipStream_t) { return hipErrorNotSupported; }
+hipError_t launch_bwd_dkv1_mfma(const BwdParams& p, hipStream_t stream) {
+  if (!bwd_mfma_ok(p)) return hipErrorNotSupported;
+  const BwdGeo geo = base_geo(p);
+  return p.d == 64 ? launch_dkv1_d<64>(p, geo, stream) : launch_dkv1_d<128>(p, geo, stream);
+}
 hipError_t launch_bwd_dkv2_mfma(const BwdParams&, hipStream_t) { return hipErrorNotSupported; }
 
 }  // namespace sa
