@@ -17,6 +17,11 @@
 //     S^T, dP^T, dS as above (A rows q_t ⊙ k1_j, B rows dout_t ⊙ v1_j)
 //     G^T  += K2^T · dS^T,  O''^T += V2^T · bf16(P)^T     (d x t)
 //     dk1_j = Σ_h Σ_t G_t ⊙ q_t,   dv1_j = Σ_h Σ_t O''_t ⊙ dout_t
+//   dk2/dv2 pass (one wave per 32 long keys, their K2/V2 rows held as MFMA
+//   fragments; the workgroup streams every (t, h) that reaches its keys and
+//   builds that step's A_t / B_t rows (32 short keys j) in LDS)
+//     S^T = A_t · K2^T, dP^T = B_t · V2^T                (j x keys)
+//     dK2^T += A_t^T · dS^T,  dV2^T += B_t^T · bf16(P)^T  (d x keys)
 //
 // The tile machinery (LDS ring filled by global->LDS DMA, TileGeom layouts,
 // the transposing-read accumulation) is the forward kernel's (sa_mfma.h).
@@ -623,6 +628,234 @@ hipError_t launch_dkv1_d(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
   return launch_dkv1_t<D, 4, 1>(p, geo, stream);
 }
 
+
+// ---------------------------------------------------------------------------
+// dk2, dv2: a workgroup of 4 waves owns 128 consecutive long keys of one KV
+// group; wave w's 32 keys are kw = k0 + 32w + lane % 32.  It walks the steps
+// (t, h) for t = k0 .. k0 + 127 + wl - 1 (every query whose long window can
+// reach a key of the block) and h over the group's heads.  Per step the waves
+// build A_t (rows j = t - 31 .. t: bf16(q_th ⊙ k1_j)) and B_t (bf16(dout_th ⊙
+// v1_j)) in LDS, 8 rows each; tiles are double-buffered, one barrier per
+// step.  Wave 0 stages each step's q, dout, k1_t and v1_t rows with one
+// full-wave DMA two steps ahead; the k1 / v1 rows of earlier queries come
+// from a 64-row ring (row j at slot j % 64) into which wave 0 copies each
+// staged k1_t / v1_t.  Covers ws <= 32 (one 32-row block of short keys).
+constexpr int kKvRing = 64;
+
+template <int D>
+__global__ __launch_bounds__(256, 1) void bwd_dkv2_mfma_kernel(BwdParams p, int nblocks) {
+  using OPS = BwdOps<D>;
+  constexpr int RS = 2 * D + 32;           // A / B tile row stride (padded: row and transposing reads)
+  constexpr int TILE = 32 * RS;            // one A or B tile
+  constexpr int RB = 2 * D;                // ring / staging row (bytes)
+  constexpr int kRowLanes = RB / 16;       // lanes per row in a DMA instruction
+  static_assert(4 * RB <= 1024, "one DMA instruction stages the 4 rows of a step");
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  char* const tiles = lds;                        // [2 buffers][A, B]
+  char* const ring = tiles + 4 * TILE;            // [64 slots][k1 row, v1 row]
+  char* const stage = ring + kKvRing * 2 * RB;    // [3][q row, dout row, k1_t row, v1_t row] (1 KB each)
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5, n = lane & 31;
+  const int lb = xcd_remap(blockIdx.x, nblocks);
+  const int kblocks = (p.tokens + 127) / 128;
+  const int kb = lb % kblocks;
+  const int g = lb / kblocks;
+  const int k0 = kb * 128;
+  const int last = p.tokens - 1;
+  const int kw = k0 + 32 * wid + n;  // this lane's key (column of the C layout)
+  const int kwc = min(kw, last);
+  const bool kvalid = kw < p.tokens;
+  const int G = p.group;
+  const int64_t kvg_k = (int64_t)g * p.k_sh, kvg_v = (int64_t)g * p.v_sh;
+
+  // K2 / V2 rows of the wave's keys as B operands (k = d): lane (n, half)
+  // holds d = 16t + 8*half .. +7 of key kw.
+  const bf16* k2r = (const bf16*)p.k2 + (int64_t)kwc * p.k_st + kvg_k;
+  const bf16* v2r = (const bf16*)p.v2 + (int64_t)kwc * p.v_st + kvg_v;
+  bf16x8 kf[D / 16], vf[D / 16];
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t) {
+    kf[t] = *(const bf16x8*)(k2r + 16 * t + 8 * half);
+    vf[t] = *(const bf16x8*)(v2r + 16 * t + 8 * half);
+  }
+  floatx16 dk[D / 32], dv[D / 32];
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) dk[i] = dv[i] = floatx16{};
+
+  // step s <-> (t = tfirst + s / G, h = g*G + s % G)
+  const int tfirst = k0;
+  const int tlast = min(last, k0 + 127 + p.wl - 1);
+  const int nsteps = (tlast - tfirst + 1) * G;
+
+  // Wave 0 stages step st: lane -> row (lane / kRowLanes) % 4, 16-byte segment
+  // lane % kRowLanes (rows q, dout, k1_t, v1_t); every lane active, one instruction.
+  auto dma_step = [&](int st) {
+    if (wid != 0 || st >= nsteps) return;
+    const int t = tfirst + st / G, h = g * G + st % G;
+    const int row = (lane / kRowLanes) & 3, seg = lane % kRowLanes;
+    const bf16* src;
+    if (row == 0) src = (const bf16*)p.q + (int64_t)t * p.q_st + (int64_t)h * p.q_sh;
+    else if (row == 1) src = (const bf16*)p.dout + (int64_t)t * p.do_st + (int64_t)h * p.do_sh;
+    else if (row == 2) src = (const bf16*)p.k1 + (int64_t)t * p.k_st + kvg_k;
+    else src = (const bf16*)p.v1 + (int64_t)t * p.v_st + kvg_v;
+    dma16(src + seg * 8, stage + (st % 3) * 1024);
+  };
+  // wave 0 copies the staged k1_t / v1_t rows of step st into ring slot t % 64
+  auto to_ring = [&](int st) {
+    if (wid != 0 || st >= nsteps) return;
+    const int t = tfirst + st / G;
+    if (lane < 2 * kRowLanes) {
+      const uint4 x = *(const uint4*)(stage + (st % 3) * 1024 + 2 * RB + 16 * lane);
+      *(uint4*)(ring + (t % kKvRing) * 2 * RB + 16 * lane) = x;
+    }
+  };
+
+  dma_step(0);
+  dma_step(1);
+  // the k1 / v1 rows before the first query (j = tfirst - 31 .. tfirst - 1) into the ring
+  for (int idx = tid; idx < 31 * 2 * kRowLanes; idx += 256) {
+    const int jj = idx / (2 * kRowLanes), w = idx % (2 * kRowLanes);
+    const int j = tfirst - 31 + jj;
+    if (j >= 0) {
+      const int which = w / kRowLanes, seg = w % kRowLanes;  // 0: k1, 1: v1
+      const bf16* src = which == 0 ? (const bf16*)p.k1 + (int64_t)j * p.k_st + kvg_k
+                                   : (const bf16*)p.v1 + (int64_t)j * p.v_st + kvg_v;
+      *(uint4*)(ring + (j % kKvRing) * 2 * RB + which * RB + 16 * seg) = *(const uint4*)(src + seg * 8);
+    }
+  }
+  wait_vmcnt<0>();
+  block_barrier();
+
+  // form A / B rows of step st into tile buffer b: wave w builds rows 8w .. 8w+7;
+  // row 31 (j = t) comes from the stage, earlier rows from the ring
+  auto form = [&](int st, int b) {
+    const int t = tfirst + st / G;
+    const char* sg_row = stage + (st % 3) * 1024;
+    char* At = tiles + b * 2 * TILE;
+    char* Bt = At + TILE;
+    constexpr int SEGS = D / 8;  // 16-byte segments per row
+#pragma unroll
+    for (int u = 0; u < 8 * SEGS / 64; ++u) {
+      const int idx = u * 64 + lane;
+      const int i = 8 * wid + idx / SEGS, sg = idx % SEGS;  // tile row, segment
+      const int j = max(t - 31 + i, 0);
+      const char* kvrow = j == t ? sg_row + 2 * RB : ring + (j % kKvRing) * 2 * RB;
+      const bf16x8 qv = *(const bf16x8*)(sg_row + 16 * sg);
+      const bf16x8 gv = *(const bf16x8*)(sg_row + RB + 16 * sg);
+      const bf16x8 kv = *(const bf16x8*)(kvrow + 16 * sg);
+      const bf16x8 vv = *(const bf16x8*)(kvrow + RB + 16 * sg);
+      bf16x8 a, bb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        a[e] = (bf16)((float)qv[e] * (float)kv[e]);
+        bb[e] = (bf16)((float)gv[e] * (float)vv[e]);
+      }
+      *(bf16x8*)(At + i * RS + 16 * sg) = a;
+      *(bf16x8*)(Bt + i * RS + 16 * sg) = bb;
+    }
+  };
+
+  const float sl2s = p.scale * kLog2e;
+  // sequence tracking for t (dense: boundary every seqlen; varlen: cu walk)
+  int seq = 0;
+  if (p.cu != nullptr) {
+    int lo = 0, hi = p.num_seqs - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (p.cu[mid] <= tfirst) lo = mid;
+      else hi = mid - 1;
+    }
+    seq = lo;
+  }
+  to_ring(0);
+  form(0, 0);
+  for (int st = 0; st < nsteps; ++st) {
+    // wave 0: the rows of step st+1 have landed (step st+2's may be in flight)
+    if (wid == 0) {
+      dma_step(st + 2);
+      if (st + 2 < nsteps) wait_vmcnt<1>();
+      else wait_vmcnt<0>();
+    }
+    block_barrier();  // tiles of st formed, ring rows up to t(st) copied; rows of st+1 staged; buffer (st+1)%2 free
+    if (st + 1 < nsteps) {
+      to_ring(st + 1);  // slot t(st+1) % 64 is read only from the next iteration on
+      form(st + 1, (st + 1) & 1);
+    }
+
+    const int t = tfirst + st / G, h = g * G + st % G;
+    int s0;
+    if (p.cu == nullptr) {
+      s0 = (t / p.seqlen) * p.seqlen;
+    } else {
+      while (seq + 1 < p.num_seqs && p.cu[seq + 1] <= t) ++seq;
+      s0 = min(max(p.cu[seq], 0), t);
+    }
+    s0 = __builtin_amdgcn_readfirstlane(s0);
+    const int64_t th = (int64_t)t * p.hq + h;
+    const float lse2 = p.lse[(int64_t)t * p.lse_st + h] * kLog2e;
+    const bool single = t == s0 || (p.ws == 1 && p.wl == 1);
+    const float dpm = single ? 0.f : p.scale;
+    const float dsm = single ? p.dl[th] * p.scale : -p.delta[th] * p.scale;
+    // validity: key kw in [max(s0, t - wl + 1), t]; row i (j = t - 31 + i) in [max(s0, t - ws + 1), t]
+    const bool kok = kvalid && kw <= t && kw >= max(s0, t - p.wl + 1);
+    const int ilo = max(s0, t - p.ws + 1) - (t - 31);
+    const char* At = tiles + (st & 1) * 2 * TILE;
+    const char* Bt = At + TILE;
+    const floatx16 sv = OPS::template rows_x<RS>(At, 0, lane, kf);  // C[j][key]
+    const floatx16 dp = OPS::template rows_x<RS>(Bt, 0, lane, vf);
+    uint32_t pp[8], pd[8];
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) {
+      const int i0 = 8 * (e >> 2) + 4 * half + (e & 3), i1 = i0 + 1;
+      const bool ok0 = kok && i0 >= ilo, ok1 = kok && i1 >= ilo;
+      const float p0 = ok0 ? fast_exp2(fmaf(sv[e], sl2s, -lse2)) : 0.f;
+      const float p1 = ok1 ? fast_exp2(fmaf(sv[e + 1], sl2s, -lse2)) : 0.f;
+      pp[e >> 1] = pack_bf16(p0, p1);
+      pd[e >> 1] = pack_bf16(p0 * fmaf(dp[e], dpm, dsm), p1 * fmaf(dp[e + 1], dpm, dsm));
+    }
+    const bf16x8 db0 = __builtin_bit_cast(bf16x8, u32x4{pd[0], pd[1], pd[2], pd[3]});
+    const bf16x8 db1 = __builtin_bit_cast(bf16x8, u32x4{pd[4], pd[5], pd[6], pd[7]});
+    OPS::template tr_acc<RS>(dk, At, 0, lane, db0, db1);  // dK2^T += A_t^T · dS^T
+    const bf16x8 pb0 = __builtin_bit_cast(bf16x8, u32x4{pp[0], pp[1], pp[2], pp[3]});
+    const bf16x8 pb1 = __builtin_bit_cast(bf16x8, u32x4{pp[4], pp[5], pp[6], pp[7]});
+    OPS::template tr_acc<RS>(dv, Bt, 0, lane, pb0, pb1);  // dV2^T += B_t^T · P^T
+  }
+
+  // write: acc[db] holds d = 32*db + acc_row(r, half) of key kw
+  if (kvalid) {
+    bf16* dkr = (bf16*)p.dk2 + (int64_t)kw * p.dk_st + (int64_t)g * p.dk_sh;
+    bf16* dvr = (bf16*)p.dv2 + (int64_t)kw * p.dv_st + (int64_t)g * p.dv_sh;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d = 32 * db + 8 * q4 + 4 * half;
+        bf16x4 a, b;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          a[e] = (bf16)dk[db][4 * q4 + e];
+          b[e] = (bf16)dv[db][4 * q4 + e];
+        }
+        *(bf16x4*)(dkr + d) = a;
+        *(bf16x4*)(dvr + d) = b;
+      }
+  }
+}
+
+template <int D>
+hipError_t launch_dkv2_d(const BwdParams& p, hipStream_t stream) {
+  constexpr int RS = 2 * D + 32, RB = 2 * D;
+  const size_t lds = (size_t)4 * 32 * RS + (size_t)kKvRing * 2 * RB + 3 * 1024;
+  const int nblocks = (p.tokens + 127) / 128 * p.hk;
+  auto kern = bwd_dkv2_mfma_kernel<D>;
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(nblocks), dim3(256), lds, stream, p, nblocks);
+  return hipGetLastError();
+}
+
 // bf16, DK == DV in {64, 128}, 16-byte aligned rows.
 bool bwd_mfma_ok(const BwdParams& p) {
   if (!p.mfma) return false;
@@ -655,6 +888,9 @@ hipError_t launch_bwd_dkv1_mfma(const BwdParams& p, hipStream_t stream) {
   const BwdGeo geo = base_geo(p);
   return p.d == 64 ? launch_dkv1_d<64>(p, geo, stream) : launch_dkv1_d<128>(p, geo, stream);
 }
-hipError_t launch_bwd_dkv2_mfma(const BwdParams&, hipStream_t) { return hipErrorNotSupported; }
+hipError_t launch_bwd_dkv2_mfma(const BwdParams& p, hipStream_t stream) {
+  if (!bwd_mfma_ok(p) || p.ws > 32) return hipErrorNotSupported;
+  return p.d == 64 ? launch_dkv2_d<64>(p, stream) : launch_dkv2_d<128>(p, stream);
+}
 
 }  // namespace sa
