@@ -5,11 +5,12 @@ Prints ONE JSON line.  Headline (``value``): bf16 2-simplicial prefill
 forward throughput in TFLOP/s on the north-star shape (B=2, H=16, S=8192,
 D=128, long window w1=512, short window w2=32), effective FLOPs
 4*B*H*S*w1*w2*D, with inputs resident in HBM.  The same line carries the
-paged decode leg (tok/s and HBM GB/s), the roofline
+paged decode leg (tok/s and HBM GB/s), the backward leg
+(forward + backward through autograd on the same prefill shape), the roofline
 fraction of the dominant kernel and the CPU baseline (the oracle timed on
 this host's cores on a bounded sample of the same workload).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--legs prefill,decode,cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--legs prefill,decode,backward,cpu]
 """
 
 from __future__ import annotations
@@ -35,7 +36,8 @@ def _args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--decode-steps", type=int, default=200)
-    ap.add_argument("--legs", default="prefill,decode,cpu")
+    ap.add_argument("--bwd-steps", type=int, default=10)
+    ap.add_argument("--legs", default="prefill,decode,backward,cpu")
     ap.add_argument("--workload", default="NS", help="prefill workload: NS, C2, C3, C4")
     ap.add_argument("--cpu-positions", type=int, default=256)
     ap.add_argument("--cpu-decode-tokens", type=int, default=16)
@@ -200,6 +202,43 @@ def decode_cpu_leg(args, cfg, inp):
     }
 
 
+def backward_leg(args, fwd_ms):
+    """Forward + backward (torch.autograd through the library's backward) on the
+    prefill workload; nominal backward FLOPs = 2x the forward's (the reference
+    counts 12*H*D*triples for forward + backward, limite_cost.py:69-73)."""
+    import torch
+    from archlab_amd import simplicial_attention, simplicial_varlen_attention
+    from archlab_amd import workloads as W
+    cfg = {"NS": W.NS, "C2": W.C2, "C3": W.C3, "C4": W.C4}[args.workload]
+    dev = torch.device("cuda:0")
+    q, k1, k2, v1, v2, cu = W.prefill_inputs(cfg, device=dev)
+    xs = [t.detach().requires_grad_(True) for t in (q, k1, k2, v1, v2)]
+    g = torch.Generator("cpu").manual_seed(7)
+    dy = torch.randn(q.shape[:-1] + (v1.shape[-1],), generator=g).to(cfg.dtype).to(dev)
+
+    def fwd():
+        if cu is None:
+            return simplicial_attention(*xs, cfg.w2, cfg.w1, scale=1.0)
+        return simplicial_varlen_attention(*xs, cu, cfg.w2, cfg.w1, scale=1.0)
+
+    def step():
+        return torch.autograd.grad(fwd(), xs, dy)
+    mean_ms, med_ms, _ = _time_kernel(step, args.bwd_steps, 3)
+    if fwd_ms is None:
+        with torch.no_grad():
+            fwd_ms, _, _ = _time_kernel(fwd, args.bwd_steps, 3)
+    bwd_ms = mean_ms - fwd_ms
+    flops = 2.0 * W.prefill_flops(cfg)
+    del xs, dy, q, k1, k2, v1, v2
+    torch.cuda.empty_cache()
+    return {
+        "workload": cfg.name, "fwd_bwd_ms": mean_ms, "fwd_ms": fwd_ms, "bwd_ms": bwd_ms,
+        "bwd_flops": flops, "bwd_tflops": flops / (bwd_ms * 1e-3) / 1e12,
+        "bwd_frac_of_peak": flops / (bwd_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+        "kernels": "bwd_dq_mfma_kernel, bwd_dkv1_mfma_kernel, bwd_dkv2_mfma_kernel (+ bwd_delta_kernel)",
+    }
+
+
 def copy_leg(args):
     """Plain device copy of a known byte count (1 GiB read + 1 GiB written per
     call): the calibration kernel for the FETCH_SIZE / WRITE_SIZE counters."""
@@ -291,6 +330,9 @@ def main():
             out["ms_per_step"] = round(dec["us_per_step"] / 1e3, 5)
             out["config"] = {"workload": dec["workload"]}
             out["roofline"] = dec["roofline"]
+    if "backward" in legs:
+        bwd = backward_leg(args, pre["ms"] if pre is not None else None)
+        out["backward"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in bwd.items()}
     if "copy" in legs:
         out["copy_calibration"] = copy_leg(args)
     if "cpu" in legs:

@@ -62,19 +62,41 @@ __device__ __forceinline__ bool single_pair(const BwdParams& p, int t, int start
   return t == start || (p.ws == 1 && p.wl == 1);
 }
 
+// delta = dout · out - dlse per (token, head): 16 lanes per row, each lane
+// 16 bytes of dout and out per step, reduced over the 16 lanes.
 template <typename T>
 __global__ __launch_bounds__(kBwdThreads) void bwd_delta_kernel(BwdParams p) {
-  const int64_t th = (int64_t)blockIdx.x * kBwdThreads + threadIdx.x;
-  if (th >= (int64_t)p.tokens * p.hq) return;
-  const int t = (int)(th / p.hq), h = (int)(th % p.hq);
+  constexpr int E = 16 / sizeof(T);  // elements per 16-byte load
+  const int64_t th = (int64_t)blockIdx.x * (kBwdThreads / 16) + threadIdx.x / 16;
+  const int l = threadIdx.x & 15;
+  const bool ok = th < (int64_t)p.tokens * p.hq;
+  const int64_t tc = ok ? th : 0;
+  const int t = (int)(tc / p.hq), h = (int)(tc % p.hq);
   const T* o = (const T*)p.out + (int64_t)t * p.o_st + (int64_t)h * p.o_sh;
   const T* g = (const T*)p.dout + (int64_t)t * p.do_st + (int64_t)h * p.do_sh;
   float s = 0.f;
-  for (int e = 0; e < p.dv; ++e) s = fmaf(ld(g + e), ld(o + e), s);
-  // an LSE gradient adds dlse * P to dL/ds: folded in as delta - dlse
-  const float gl = p.dlse ? p.dlse[(int64_t)t * p.dlse_st + h] : 0.f;
-  p.delta[th] = s - gl;
-  p.dl[th] = gl;
+  if (ok) {
+    if (p.dv % E == 0 && ((uintptr_t)o % 16) == 0 && ((uintptr_t)g % 16) == 0) {
+      for (int e = l * E; e < p.dv; e += 16 * E) {
+        const uint4 ov = *(const uint4*)(o + e), gv = *(const uint4*)(g + e);
+        const T* ot = (const T*)&ov;
+        const T* gt = (const T*)&gv;
+#pragma unroll
+        for (int u = 0; u < E; ++u) s = fmaf(ld(gt + u), ld(ot + u), s);
+      }
+    } else {
+      for (int e = l; e < p.dv; e += 16) s = fmaf(ld(g + e), ld(o + e), s);
+    }
+  }
+  // sum over the 16 lanes of the row (xor shuffles stay inside the 16-lane group)
+#pragma unroll
+  for (int m = 8; m > 0; m >>= 1) s += __shfl_xor(s, m, 16);
+  if (ok && l == 0) {
+    // an LSE gradient adds dlse * P to dL/ds: folded in as delta - dlse
+    const float gl = p.dlse ? p.dlse[(int64_t)t * p.dlse_st + h] : 0.f;
+    p.delta[th] = s - gl;
+    p.dl[th] = gl;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -511,8 +533,9 @@ size_t prefill_bwd_workspace_bytes(const sa_prefill_bwd_args* a) { return 2 * bw
 template <typename T>
 static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
   const int64_t nth = (int64_t)p.tokens * p.hq;
-  hipLaunchKernelGGL(bwd_delta_kernel<T>, dim3((unsigned)((nth + kBwdThreads - 1) / kBwdThreads)), dim3(kBwdThreads),
-                     0, stream, p);
+  constexpr int kRowsPerBlock = kBwdThreads / 16;
+  hipLaunchKernelGGL(bwd_delta_kernel<T>, dim3((unsigned)((nth + kRowsPerBlock - 1) / kRowsPerBlock)),
+                     dim3(kBwdThreads), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   struct K {
