@@ -16,6 +16,12 @@
 // ring of P + 1 slots by direct global->LDS DMA, P tiles ahead of use, one
 // barrier per step.
 //
+// Score and value widths up to 128: the ring (P = 1) is the only LDS the
+// workgroup holds, so three workgroups share a CU (three waves per SIMD hide
+// each other's barrier and load latencies); the A rows and the epilogue's v1
+// rows are read from global memory.  Widths of 256 run one wave per SIMD and
+// stage the short window in one more LDS slot instead.
+//
 // The joint softmax is kept per A row (running max / sum); the epilogue merges
 // the rows with their log-sum-exp weights and applies v1:
 //     out = sum_j w_j (v1_j ⊙ O_j) / sum_j w_j z_j,   w_j = exp(m_j - max m).
@@ -52,33 +58,32 @@ struct PrefillParams {
 };
 
 #ifndef SA_PREFILL_WAVES_PER_SIMD
-#define SA_PREFILL_WAVES_PER_SIMD 2
+#define SA_PREFILL_WAVES_PER_SIMD 3
 #endif
 #ifndef SA_PREFILL_DEPTH
-#define SA_PREFILL_DEPTH 2
-#endif
-#ifndef SA_PREFILL_WAVES
-#define SA_PREFILL_WAVES 4
+#define SA_PREFILL_DEPTH 1
 #endif
 
 template <int DK, int DV, int NQ, int NH, int P>
 __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREFILL_WAVES_PER_SIMD)) void prefill_mfma_kernel(
     PrefillParams p) {
-  static_assert(NQ * NH == 4 || NQ * NH == 8, "4 or 8 waves per block");
+  static_assert(NQ * NH == 4, "4 waves per block");
   static_assert(P >= 1 && P <= 4, "prefetch depth");
   constexpr int NW = NQ * NH;
   constexpr int ROWS = kChunk + NQ - 1;  // tile rows: one chunk of all NQ queries
   using G = TileGeom<DK, DV, ROWS, NW>;
-  static_assert(NW * G::RSK <= G::kInstrV * 1024, "the q rows fit the short slot's V region");
+  // short window staged in an LDS slot (widths of 256) or read from global memory
+  constexpr bool kSlot = DK >= 256 || DV >= 256;
+  static_assert(!kSlot || NW * G::RSK <= G::kInstrV * 1024, "the q rows fit the short slot's V region");
   constexpr int R = P + 1;  // ring slots for the long-axis tiles
   constexpr int NI = G::NI;
   // the pipelined loop holds a second score tile: registers allow it up to DK = DV = 128
   constexpr bool kPipelined = DK <= 128 && DV <= 128 && P >= 2;
   extern __shared__ __attribute__((aligned(16))) char lds[];
-  // One more slot after the ring holds the short window of the pass: its K
-  // region takes the k1 rows and (in its V region) the q rows of the NW waves
-  // at the start of the pass; the v1 rows replace the q rows during the last
-  // chunk.  All of it arrives by DMA, 1 KB per instruction.
+  // kSlot: one more slot after the ring holds the short window of the pass:
+  // its K region takes the k1 rows and (in its V region) the q rows of the NW
+  // waves at the start of the pass; the v1 rows replace the q rows during the
+  // last chunk.  All of it arrives by DMA, 1 KB per instruction.
   char* const sslot = lds + R * G::SLOT;
 
   const int tid = threadIdx.x;
@@ -187,17 +192,25 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
   for (int r = 0; r < p.nr; ++r) {
     const int j = t - 32 * r - n;  // this lane's short-axis key
     const bool row_ok = qvalid && j >= lo1;
+    const int jc = min(max(j, 0), last);  // a readable row for every lane
     // Pass prologue: the short window (k1 rows, q rows) and the first P tiles
     // go out together; A is formed once the short window has landed.
     const int kbs = t0 - 31 - 32 * r;  // short-slot row 0 (short key of tile row 0)
-    dma_tile(std::integral_constant<int, 1>{}, sslot, kbs, p.k1, p.v1);
-    dma_q();
+    const int srow = qo + 31 - n;      // this lane's short key j in the short slot
+    if constexpr (kSlot) {
+      dma_tile(std::integral_constant<int, 1>{}, sslot, kbs, p.k1, p.v1);
+      dma_q();
+    }
 #pragma unroll
     for (int e = 0; e < P; ++e) issue(c0 + e);  // unconditional: static count for the wait below
-    wait_vmcnt<P * NI>();
-    block_barrier();
-    const int srow = qo + 31 - n;  // this lane's short key j in the short slot
-    rb.form_a_lds(sslot + srow * G::RSK, sslot + G::VOFF + wid * G::RSK, row_ok, half, p.q_neg != 0);
+    if constexpr (kSlot) {
+      wait_vmcnt<P * NI>();
+      block_barrier();
+      rb.form_a_lds(sslot + srow * G::RSK, sslot + G::VOFF + wid * G::RSK, row_ok, half, p.q_neg != 0);
+    } else {
+      rb.form_a(p.q + (int64_t)min(t, last) * p.q_st + (int64_t)h * p.q_sh, p.k1 + (int64_t)jc * k_st + k_g,
+                row_ok, half, p.q_neg != 0);
+    }
     rb.reset();
     if constexpr (kPipelined) {
       // Software-pipelined chunk loop: iteration c needs K of chunk c+1 and
@@ -232,10 +245,10 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
                                                  p.sl2);
         }
         begin_chunk(c, s, cmax);
-        dma_tile(std::integral_constant<int, 2>{}, sslot, kbs, p.k1, p.v1);  // v1 rows for the epilogue
+        if constexpr (kSlot) dma_tile(std::integral_constant<int, 2>{}, sslot, kbs, p.k1, p.v1);  // v1 rows
         const char* slot = lds + (c % R) * G::SLOT;
         rb.template step<G::RSK, G::RSV, false>(s, cmax, slot, slot + G::VOFF, qo, lane, p.sl2);
-      } else {
+      } else if constexpr (kSlot) {
         dma_tile(std::integral_constant<int, 2>{}, sslot, kbs, p.k1, p.v1);
       }
     } else {
@@ -243,7 +256,8 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
         wait_tiles<NI, P>(min(P - 1, p.nc - 1 - c));
         block_barrier();  // tile c complete for every wave; slot of tile c-1 free
         if (c + P < p.nc) issue(c + P);
-        if (c + 1 == p.nc) dma_tile(std::integral_constant<int, 2>{}, sslot, kbs, p.k1, p.v1);  // v1 rows
+        if constexpr (kSlot)
+          if (c + 1 == p.nc) dma_tile(std::integral_constant<int, 2>{}, sslot, kbs, p.k1, p.v1);  // v1 rows
         // Unconditional: a wave without valid keys in this step gets an empty
         // key range (every p = 0, an exact no-op).  A branch here would give
         // the accumulators two incoming values at the loop latch, which the
@@ -255,9 +269,10 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
                                           active ? max(lo2 - kfirst, 0) : kChunk,
                                           active ? min(t - kfirst, kChunk - 1) : -1);
       }
-      if (c0 >= p.nc) dma_tile(std::integral_constant<int, 2>{}, sslot, kbs, p.k1, p.v1);
+      if constexpr (kSlot)
+        if (c0 >= p.nc) dma_tile(std::integral_constant<int, 2>{}, sslot, kbs, p.k1, p.v1);
     }
-    wait_vmcnt<0>();  // this wave's part of the v1 rows
+    if constexpr (kSlot) wait_vmcnt<0>();  // this wave's part of the v1 rows
     block_barrier();  // ring reads done (LDS reused below); v1 rows complete
 
     // ---- epilogue of this pass: merge the 32 rows of the wave
@@ -267,7 +282,8 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
     const float wgt = (row_ok && Mw > -INFINITY) ? fast_exp2(mrow - Mw) : 0.f;
     const float Zw = half_sum(wgt * zrow);
     float* red = (float*)lds + wid * (64 * 36);  // [64 d][36] per wave (ring region)
-    const char* v1s = sslot + G::VOFF + srow * G::RSV;  // this lane's v1 row
+    // this lane's v1 row
+    const char* v1s = kSlot ? sslot + G::VOFF + srow * G::RSV : (const char*)(p.v1 + (int64_t)jc * v_st + v_g);
     const float Mn = fmaxf(Mrun, Mw);
     const float a0 = Mrun > -INFINITY ? fast_exp2(Mrun - Mn) : 0.f;
     const float a1 = Mw > -INFINITY ? fast_exp2(Mw - Mn) : 0.f;
@@ -347,7 +363,8 @@ static hipError_t launch_prefill_mfma(const PrefillParams& base_p, hipStream_t s
   p.nblocks = p.qblocks * p.hk * p.hsub;
   constexpr int NW = NQ * NH;
   using G = TileGeom<DK, DV, kChunk + NQ - 1, NW>;
-  size_t lds = (size_t)(P + 2) * G::SLOT;  // P + 1 ring slots + the short-window slot
+  constexpr bool kSlot = DK >= 256 || DV >= 256;
+  size_t lds = (size_t)(P + (kSlot ? 2 : 1)) * G::SLOT;  // P + 1 ring slots (+ the short-window slot)
   const size_t red = (size_t)NW * 64 * 36 * sizeof(float);
   if (lds < red) lds = red;
   auto kern = prefill_mfma_kernel<DK, DV, NQ, NH, P>;
@@ -357,8 +374,9 @@ static hipError_t launch_prefill_mfma(const PrefillParams& base_p, hipStream_t s
   return hipGetLastError();
 }
 
-// Prefetch depth per configuration: the ring is sized to leave room for two
-// workgroups per CU (<= 80 KB) where registers allow it.
+// Prefetch depth per configuration: widths up to 128 keep one tile in flight
+// per workgroup with three workgroups per CU (40 KB of LDS each); widths of
+// 256 keep two, one workgroup per CU.
 template <int DK, int DV>
 static hipError_t dispatch_prefill_mfma_d(const PrefillParams& p, hipStream_t stream) {
   const int G = p.group;
@@ -366,11 +384,6 @@ static hipError_t dispatch_prefill_mfma_d(const PrefillParams& p, hipStream_t st
     if (G % 4 == 0) return launch_prefill_mfma<DK, DV, 1, 4, 2>(p, stream);
     if (G % 2 == 0) return launch_prefill_mfma<DK, DV, 2, 2, 2>(p, stream);
     return launch_prefill_mfma<DK, DV, 4, 1, 2>(p, stream);
-  } else if constexpr (SA_PREFILL_WAVES == 8) {
-    // one 8-wave workgroup per CU: a tile serves twice the queries
-    if (G % 4 == 0) return launch_prefill_mfma<DK, DV, 2, 4, 3>(p, stream);
-    if (G % 2 == 0) return launch_prefill_mfma<DK, DV, 4, 2, 3>(p, stream);
-    return launch_prefill_mfma<DK, DV, 8, 1, 3>(p, stream);
   } else {
     constexpr int P = SA_PREFILL_DEPTH;
     if (G % 4 == 0) return launch_prefill_mfma<DK, DV, 1, 4, P>(p, stream);
