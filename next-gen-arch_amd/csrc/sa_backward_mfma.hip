@@ -120,7 +120,7 @@ __global__ __launch_bounds__(64 * NQ * NH, 2) void bwd_dq_mfma_kernel(BwdParams 
   static_assert(NQ * NH == 4, "4 waves per block");
   constexpr int NW = NQ * NH;
   constexpr int ROWS = kChunk + NQ - 1;
-  using G = TileGeom<D, D, ROWS, NW>;
+  using G = TileGeom<D, D, ROWS, NW, 32, 32>;
   using OPS = BwdOps<D>;
   constexpr int R = P + 1;
   constexpr int NI = G::NI;
@@ -329,7 +329,7 @@ hipError_t launch_dq_t(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
   geo.hsub = p.group / NH;
   geo.nblocks = geo.qblocks * p.hk * geo.hsub;
   constexpr int NW = NQ * NH;
-  using G = TileGeom<D, D, kChunk + NQ - 1, NW>;
+  using G = TileGeom<D, D, kChunk + NQ - 1, NW, 32, 32>;
   const size_t qslot = ((size_t)2 * NW * G::RSK + 1023) / 1024 * 1024;
   const size_t ring = (size_t)(P + 1) * G::SLOT, red = (size_t)NW * 64 * 36 * sizeof(float);
   const size_t lds = (ring > red ? ring : red) + G::SLOT + qslot;
@@ -363,7 +363,7 @@ __global__ __launch_bounds__(64 * NQ * NH, (D >= 128 ? 1 : 2)) void bwd_dkv1_mfm
   static_assert(NQ == 4 && NH == 1, "4 keys per block, one head at a time");
   constexpr int NW = NQ * NH;
   constexpr int ROWS = kChunk + NQ - 1;
-  using G = TileGeom<D, D, ROWS, NW>;
+  using G = TileGeom<D, D, ROWS, NW, 32, 32>;
   using OPS = BwdOps<D>;
   constexpr int R = P + 1;
   constexpr int NI = G::NI;
@@ -612,7 +612,7 @@ hipError_t launch_dkv1_t(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
   geo.hsub = p.group / NH;
   geo.nblocks = geo.qblocks * p.hk;
   constexpr int NW = NQ * NH;
-  using G = TileGeom<D, D, kChunk + NQ - 1, NW>;
+  using G = TileGeom<D, D, kChunk + NQ - 1, NW, 32, 32>;
   const size_t kslot = ((size_t)2 * NW * G::RSK + 1023) / 1024 * 1024;
   const size_t ring = (size_t)(P + 1) * G::SLOT, red = (size_t)NW * 64 * 36 * sizeof(float);
   const size_t lds = (ring > red ? ring : red) + G::SLOT + kslot;

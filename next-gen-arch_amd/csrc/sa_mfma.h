@@ -11,7 +11,7 @@
 //
 // DK is the score width (q, k1, k2) and DV the value width (v1, v2, out); the
 // reference's determinant scores use DK = 2 * DV.  LDS tiles: K [rows][DK]
-// and V [rows][DV] bf16, row-major with a 32-byte pad per row (see TileGeom).
+// and V [rows][DV] bf16, row-major with a pad per row (see TileGeom).
 //
 // Tiles are filled with global_load_lds_dwordx4 (16 bytes per lane straight
 // into LDS, no staging registers); one instruction fills 1 KB of LDS.
@@ -31,17 +31,21 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
 
 // LDS tile geometry.  The K tile is [rows][DK] bf16 with a row stride of
-// 2DK + 32 bytes, the V tile [rows][DV] with 2DV + 32: the 32-byte pad shifts
-// consecutive rows by 8 banks, which keeps both the 16-byte K reads (32 rows,
-// one segment) and the 8-byte transposing V reads (4 rows x 32 bytes per 16
-// lanes) free of bank conflicts, and every read address is a per-lane base
-// plus an immediate.
-template <int DK, int DV, int ROWS_T, int NW, int PAD = 32>
+// 2DK + PADK bytes, the V tile [rows][DV] with 2DV + PADV.  LDS has 64 banks
+// of 4 bytes; a ds_read_b128 serves 16 lanes per cycle and a
+// ds_read_b64_tr_b16 32 lanes (measured with SQ_LDS_BANK_CONFLICT on this
+// GPU).  The K reads put 16 consecutive rows (16 bytes each) in one cycle: a
+// 16-byte pad moves consecutive rows by 4 banks, so the 16 rows cover all 64
+// banks once.  The transposing V reads put 4 rows x 64 bytes in one cycle: a
+// 64-byte pad moves consecutive rows by 16 banks, again 64 distinct banks.
+// (A 32-byte pad on both gave 2-way conflicts on both.)  Every read address
+// is a per-lane base plus an immediate.
+template <int DK, int DV, int ROWS_T, int NW, int PADK = 16, int PADV = 64>
 struct TileGeom {
   static constexpr int kSegsK = DK / 8;                       // 16-byte segments per K row
   static constexpr int kSegsV = DV / 8;                       // ... per V row
-  static constexpr int RSK = 2 * DK + PAD;                    // LDS row strides (bytes)
-  static constexpr int RSV = 2 * DV + PAD;
+  static constexpr int RSK = 2 * DK + PADK;                   // LDS row strides (bytes)
+  static constexpr int RSV = 2 * DV + PADV;
   static constexpr int TBK = ROWS_T * RSK;                    // one K tile (bytes)
   static constexpr int TBV = ROWS_T * RSV;                    // one V tile
   static constexpr int kInstrK = (TBK + 1023) / 1024;         // DMA instructions per K tile
@@ -69,6 +73,13 @@ struct TileGeom {
   __device__ static __forceinline__ bool instr_is_v(int wid, int k) { return wid * NI + k >= kInstrK; }
   __device__ static __forceinline__ char* dst(char* slot, int wid, int k) { return slot + (wid * NI + k) * 1024; }
 };
+
+// Tile geometry of the forward kernels: widths of 256 keep 32-byte pads on
+// both tiles (measured faster there with one wave per SIMD), smaller widths
+// the conflict-free pads.
+template <int DK, int DV, int ROWS_T, int NW>
+using FwdGeom = std::conditional_t<(DK >= 256 || DV >= 256), TileGeom<DK, DV, ROWS_T, NW, 32, 32>,
+                                   TileGeom<DK, DV, ROWS_T, NW>>;
 
 // s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding:
 // vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).

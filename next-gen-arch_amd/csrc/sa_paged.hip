@@ -59,7 +59,7 @@ constexpr int kPosCache = 1024;  // long-window positions of one split whose row
 
 template <int D, int NW, int P>
 __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel(PagedParams p) {
-  using G = TileGeom<D, D, kChunk, NW>;
+  using G = FwdGeom<D, D, kChunk, NW>;
   using RB = RowBlock<D, D>;
   constexpr bool kPipelined = D <= 128 && P >= 2;  // second score tile fits the registers up to D = 128
   constexpr int SLOT = G::SLOT;
@@ -430,7 +430,7 @@ constexpr int kPagedDepth = SA_PAGED_DEPTH;  // tiles in flight per workgroup (2
 template <int D, int NW>
 static hipError_t launch_paged_mfma_t(PagedParams p, hipStream_t stream) {
   constexpr int P = D >= 256 ? 2 : kPagedDepth;
-  const size_t lds_ring = (size_t)(P + 1) * TileGeom<D, D, kChunk, NW>::SLOT + kPosCache * sizeof(int64_t);
+  const size_t lds_ring = (size_t)(P + 1) * FwdGeom<D, D, kChunk, NW>::SLOT + kPosCache * sizeof(int64_t);
   const size_t lds_red = (size_t)NW * 64 * 36 * sizeof(float);
   const size_t lds = lds_ring > lds_red ? lds_ring : lds_red;
   auto kern = paged_mfma_kernel<D, NW, P>;

@@ -71,7 +71,7 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
   static_assert(P >= 1 && P <= 4, "prefetch depth");
   constexpr int NW = NQ * NH;
   constexpr int ROWS = kChunk + NQ - 1;  // tile rows: one chunk of all NQ queries
-  using G = TileGeom<DK, DV, ROWS, NW>;
+  using G = FwdGeom<DK, DV, ROWS, NW>;
   // short window staged in an LDS slot (widths of 256) or read from global memory
   constexpr bool kSlot = DK >= 256 || DV >= 256;
   static_assert(!kSlot || NW * G::RSK <= G::kInstrV * 1024, "the q rows fit the short slot's V region");
@@ -362,7 +362,7 @@ static hipError_t launch_prefill_mfma(const PrefillParams& base_p, hipStream_t s
   p.hsub = p.group / NH;
   p.nblocks = p.qblocks * p.hk * p.hsub;
   constexpr int NW = NQ * NH;
-  using G = TileGeom<DK, DV, kChunk + NQ - 1, NW>;
+  using G = FwdGeom<DK, DV, kChunk + NQ - 1, NW>;
   constexpr bool kSlot = DK >= 256 || DV >= 256;
   size_t lds = (size_t)(P + (kSlot ? 2 : 1)) * G::SLOT;  // P + 1 ring slots (+ the short-window slot)
   const size_t red = (size_t)NW * 64 * 36 * sizeof(float);
