@@ -146,7 +146,12 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
       for (int k = 0; k < NI; ++k) {
         const bool is_v = G::instr_is_v(wid, k);
         if ((PART == 1 && is_v) || (PART == 2 && !is_v)) continue;
-        dma16(uniform_ptr(is_v ? vbase : kbase) + voff[k], G::dst(slot, wid, k));
+        // the empty asm keeps the 32-bit offsets from being widened outside the
+        // loop (held as 64-bit pairs they cost NI more VGPRs, which the
+        // allocator then spills)
+        uint32_t o = voff[k];
+        asm volatile("" : "+v"(o));
+        dma16(uniform_ptr(is_v ? vbase : kbase) + o, G::dst(slot, wid, k));
       }
     } else {  // tile crosses the tensor edge: clamp every row into [0, total)
 #pragma unroll
