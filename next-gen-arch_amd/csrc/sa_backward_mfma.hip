@@ -356,11 +356,14 @@ hipError_t launch_dq_d(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
 // covers keys j + 32r - wl + 1 + 32c + [0, 32).  The 4 waves share one K2/V2
 // tile of 35 rows per chunk and one slot of q / dout rows (head h, queries
 // j0 + 32r .. +34).
-// Two accumulator sets (G, O'') and both fragment sets need one wave per SIMD
-// at D = 128.
-template <int D, int NQ, int NH, int P>
-__global__ __launch_bounds__(64 * NQ * NH, (D >= 128 ? 1 : 2)) void bwd_dkv1_mfma_kernel(BwdParams p, BwdGeo geo) {
+// MODE 1: dk1 only (G), MODE 2: dv1 only (O''), in two launches: one
+// accumulator set (and, for dv1, neither the B rows nor dP) fits two waves
+// per SIMD; the S recomputation is paid twice.
+template <int D, int NQ, int NH, int P, int MODE>
+__global__ __launch_bounds__(64 * NQ * NH, 2) void bwd_dkv1_mfma_kernel(BwdParams p, BwdGeo geo) {
   static_assert(NQ == 4 && NH == 1, "4 keys per block, one head at a time");
+  constexpr bool kDK = MODE == 1, kDV = MODE == 2;
+  static_assert(kDK || kDV, "one output per launch");
   constexpr int NW = NQ * NH;
   constexpr int ROWS = kChunk + NQ - 1;
   using G = TileGeom<D, D, ROWS, NW, 32, 32>;
@@ -454,9 +457,9 @@ __global__ __launch_bounds__(64 * NQ * NH, (D >= 128 ? 1 : 2)) void bwd_dkv1_mfm
   };
 
   const float sl2s = p.scale * kLog2e;
-  float dk1run[D / 64], dv1run[D / 64];
+  float xrun[D / 64];  // dk1 (MODE 1) or dv1 (MODE 2) of this wave's key, d = 64*i + lane
 #pragma unroll
-  for (int i = 0; i < D / 64; ++i) dk1run[i] = dv1run[i] = 0.f;
+  for (int i = 0; i < D / 64; ++i) xrun[i] = 0.f;
   RowBlock<D, D> ra, rbv;  // A rows (q_t ⊙ k1_j), B rows (dout_t ⊙ v1_j)
   const int nc = (p.wl + 2 * kChunk - 2) / kChunk;  // chunks over wl + 31 keys
   dma_kv();
@@ -497,11 +500,11 @@ __global__ __launch_bounds__(64 * NQ * NH, (D >= 128 ? 1 : 2)) void bwd_dkv1_mfm
       const int srow = qo + n;  // row of query t in the row slot
       // kslot row w holds the k1 (v1: row NW + w) row of key j0 + w / NH, i.e. this wave's key
       ra.form_a_lds(rslot + srow * G::RSK, kslot + wid * G::RSK, row_ok, half, false);
-      rbv.form_a_lds(rslot + G::VOFF + srow * G::RSV, kslot + (NW + wid) * G::RSK, row_ok, half, false);
+      if constexpr (kDK) rbv.form_a_lds(rslot + G::VOFF + srow * G::RSV, kslot + (NW + wid) * G::RSK, row_ok, half, false);
 
-      floatx16 gacc[D / 32], oacc[D / 32];
+      floatx16 acc[D / 32];  // G^T (MODE 1) or O''^T (MODE 2)
 #pragma unroll
-      for (int i = 0; i < D / 32; ++i) gacc[i] = oacc[i] = floatx16{};
+      for (int i = 0; i < D / 32; ++i) acc[i] = floatx16{};
       for (int c = 0; c < nc; ++c) {
         wait_tiles<NI, P>(min(P - 1, nc - 1 - c));
         block_barrier();
@@ -512,12 +515,13 @@ __global__ __launch_bounds__(64 * NQ * NH, (D >= 128 ? 1 : 2)) void bwd_dkv1_mfm
         const int khi = min(n + p.wl - 1 - kChunk * c, kChunk - 1);
         const char* slot = lds + (c % R) * G::SLOT;
         const floatx16 sv = OPS::template rows_x<G::RSK>(slot, qo, lane, ra.a);
-        const floatx16 dp = OPS::template rows_x<G::RSV>(slot + G::VOFF, qo, lane, rbv.a);
+        floatx16 dp;
+        if constexpr (kDK) dp = OPS::template rows_x<G::RSV>(slot + G::VOFF, qo, lane, rbv.a);
         const int lo_h = klo - 4 * half, hi_h = khi - 4 * half;
         // interior chunk: every key valid for every row of the wave (uniform test)
         const bool interior = s0 <= kfirst && c >= 1 && kChunk * c <= p.wl - kChunk;
-        // P and dS straight into packed bf16 pairs (B operands of the two accumulations)
-        uint32_t pp[8], pd[8];
+        // dS (MODE 1) or P (MODE 2) straight into packed bf16 pairs (B operand)
+        uint32_t pk[8];
 #pragma unroll
         for (int e = 0; e < 16; e += 2) {
           const int kr0 = 8 * (e >> 2) + (e & 3), kr1 = kr0 + 1;
@@ -525,24 +529,21 @@ __global__ __launch_bounds__(64 * NQ * NH, (D >= 128 ? 1 : 2)) void bwd_dkv1_mfm
           const bool ok1 = row_ok && (interior || (kr1 >= lo_h && kr1 <= hi_h));
           const float p0 = ok0 ? fast_exp2(fmaf(sv[e], sl2s, -lse2)) : 0.f;
           const float p1 = ok1 ? fast_exp2(fmaf(sv[e + 1], sl2s, -lse2)) : 0.f;
-          pp[e >> 1] = pack_bf16(p0, p1);
-          pd[e >> 1] = pack_bf16(p0 * fmaf(dp[e], dpm, dsm), p1 * fmaf(dp[e + 1], dpm, dsm));
+          if constexpr (kDK) pk[e >> 1] = pack_bf16(p0 * fmaf(dp[e], dpm, dsm), p1 * fmaf(dp[e + 1], dpm, dsm));
+          else pk[e >> 1] = pack_bf16(p0, p1);
         }
-        const bf16x8 db0 = __builtin_bit_cast(bf16x8, u32x4{pd[0], pd[1], pd[2], pd[3]});
-        const bf16x8 db1 = __builtin_bit_cast(bf16x8, u32x4{pd[4], pd[5], pd[6], pd[7]});
-        OPS::template tr_acc<G::RSK>(gacc, slot, qo, lane, db0, db1);  // G^T += K2^T · dS^T
-        const bf16x8 pb0 = __builtin_bit_cast(bf16x8, u32x4{pp[0], pp[1], pp[2], pp[3]});
-        const bf16x8 pb1 = __builtin_bit_cast(bf16x8, u32x4{pp[4], pp[5], pp[6], pp[7]});
-        OPS::template tr_acc<G::RSV>(oacc, slot + G::VOFF, qo, lane, pb0, pb1);  // O''^T += V2^T · P^T
+        const bf16x8 b0 = __builtin_bit_cast(bf16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
+        const bf16x8 b1 = __builtin_bit_cast(bf16x8, u32x4{pk[4], pk[5], pk[6], pk[7]});
+        if constexpr (kDK) OPS::template tr_acc<G::RSK>(acc, slot, qo, lane, b0, b1);  // G^T += K2^T · dS^T
+        else OPS::template tr_acc<G::RSV>(acc, slot + G::VOFF, qo, lane, b0, b1);      // O''^T += V2^T · P^T
       }
       wait_vmcnt<0>();
       block_barrier();  // ring reads done (LDS reused below)
 
-      // dk1[d] += Σ_t G_t[d] q_t[d], dv1[d] += Σ_t O''_t[d] dout_t[d] over the wave's rows
+      // dk1[d] += Σ_t G_t[d] q_t[d] (MODE 1), dv1[d] += Σ_t O''_t[d] dout_t[d] (MODE 2)
       float* red = (float*)lds + wid * (64 * 36);
-#pragma unroll
-      for (int which = 0; which < 2; ++which) {
-        const char* xs = which == 0 ? rslot + srow * G::RSK : rslot + G::VOFF + srow * G::RSV;
+      {
+        const char* xs = kDK ? rslot + srow * G::RSK : rslot + G::VOFF + srow * G::RSV;
         bf16x4 xv[D / 64][2][4];
 #pragma unroll
         for (int sl = 0; sl < D / 64; ++sl)
@@ -562,7 +563,7 @@ __global__ __launch_bounds__(64 * NQ * NH, (D >= 128 ? 1 : 2)) void bwd_dkv1_mfm
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 const float x = row_ok ? (float)xv[sl][dbl][q4][e] : 0.f;
-                red[(dd + e) * 36 + n] = x * (which == 0 ? gacc[db][4 * q4 + e] : oacc[db][4 * q4 + e]);
+                red[(dd + e) * 36 + n] = x * acc[db][4 * q4 + e];
               }
             }
           }
@@ -573,8 +574,7 @@ __global__ __launch_bounds__(64 * NQ * NH, (D >= 128 ? 1 : 2)) void bwd_dkv1_mfm
             floatx4 x = row4[i];
             acc += (x[0] + x[1]) + (x[2] + x[3]);
           }
-          if (which == 0) dk1run[sl] += acc;
-          else dv1run[sl] += acc;
+          xrun[sl] += acc;
         }
       }
     }
@@ -582,32 +582,25 @@ __global__ __launch_bounds__(64 * NQ * NH, (D >= 128 ? 1 : 2)) void bwd_dkv1_mfm
 
   // sum over the NH waves of each key (heads hw), then write
   block_barrier();
-  float* sum = (float*)lds;  // [NW][2][D]
+  float* sum = (float*)lds;  // [NW][D]
 #pragma unroll
-  for (int i = 0; i < D / 64; ++i) {
-    sum[(wid * 2 + 0) * D + 64 * i + lane] = dk1run[i];
-    sum[(wid * 2 + 1) * D + 64 * i + lane] = dv1run[i];
-  }
+  for (int i = 0; i < D / 64; ++i) sum[wid * D + 64 * i + lane] = xrun[i];
   block_barrier();
   if (hw == 0 && jvalid) {
-    bf16* dk = (bf16*)p.dk1 + (int64_t)j * p.dk_st + (int64_t)g * p.dk_sh;
-    bf16* dv = (bf16*)p.dv1 + (int64_t)j * p.dv_st + (int64_t)g * p.dv_sh;
+    bf16* orow = kDK ? (bf16*)p.dk1 + (int64_t)j * p.dk_st + (int64_t)g * p.dk_sh
+                     : (bf16*)p.dv1 + (int64_t)j * p.dv_st + (int64_t)g * p.dv_sh;
 #pragma unroll
     for (int i = 0; i < D / 64; ++i) {
-      float a = 0.f, b = 0.f;
-      for (int w = 0; w < NH; ++w) {
-        a += sum[((wid + w) * 2 + 0) * D + 64 * i + lane];
-        b += sum[((wid + w) * 2 + 1) * D + 64 * i + lane];
-      }
-      dk[64 * i + lane] = (bf16)a;
-      dv[64 * i + lane] = (bf16)b;
+      float a = 0.f;
+      for (int w = 0; w < NH; ++w) a += sum[(wid + w) * D + 64 * i + lane];
+      orow[64 * i + lane] = (bf16)a;
     }
   }
 }
 
 template <int D, int NQ, int NH>
 hipError_t launch_dkv1_t(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
-  constexpr int P = D >= 128 ? 2 : 1;  // one workgroup per CU at D = 128: LDS for a deeper ring
+  constexpr int P = 1;  // two workgroups per CU (<= 80 KB of LDS each)
   geo.qblocks = (p.tokens + NQ - 1) / NQ;
   geo.hsub = p.group / NH;
   geo.nblocks = geo.qblocks * p.hk;
@@ -616,11 +609,14 @@ hipError_t launch_dkv1_t(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
   const size_t kslot = ((size_t)2 * NW * G::RSK + 1023) / 1024 * 1024;
   const size_t ring = (size_t)(P + 1) * G::SLOT, red = (size_t)NW * 64 * 36 * sizeof(float);
   const size_t lds = (ring > red ? ring : red) + G::SLOT + kslot;
-  auto kern = bwd_dkv1_mfma_kernel<D, NQ, NH, P>;
-  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3(geo.nblocks), dim3(64 * NW), lds, stream, p, geo);
-  return hipGetLastError();
+  for (auto kern : {bwd_dkv1_mfma_kernel<D, NQ, NH, P, 1>, bwd_dkv1_mfma_kernel<D, NQ, NH, P, 2>}) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3(geo.nblocks), dim3(64 * NW), lds, stream, p, geo);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 template <int D>
@@ -642,8 +638,13 @@ hipError_t launch_dkv1_d(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
 // staged k1_t / v1_t.  Covers ws <= 32 (one 32-row block of short keys).
 constexpr int kKvRing = 64;
 
-template <int D>
-__global__ __launch_bounds__(256, 1) void bwd_dkv2_mfma_kernel(BwdParams p, int nblocks) {
+// MODE 1: dK2 only, MODE 2: dV2 only (two launches).  Each holds one
+// accumulator set, and the dV2 launch neither the V2 fragments nor dP, so
+// both fit two waves per SIMD; the S recomputation is paid twice.
+template <int D, int MODE>
+__global__ __launch_bounds__(256, 2) void bwd_dkv2_mfma_kernel(BwdParams p, int nblocks) {
+  constexpr bool kDK = MODE == 1, kDV = MODE == 2;
+  static_assert(kDK || kDV, "one output per launch");
   using OPS = BwdOps<D>;
   constexpr int RS = 2 * D + 32;           // A / B tile row stride (padded: row and transposing reads)
   constexpr int TILE = 32 * RS;            // one A or B tile
@@ -674,15 +675,15 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv2_mfma_kernel(BwdParams p, int 
   // holds d = 16t + 8*half .. +7 of key kw.
   const bf16* k2r = (const bf16*)p.k2 + (int64_t)kwc * p.k_st + kvg_k;
   const bf16* v2r = (const bf16*)p.v2 + (int64_t)kwc * p.v_st + kvg_v;
-  bf16x8 kf[D / 16], vf[D / 16];
+  bf16x8 kf[D / 16], vf[kDK ? D / 16 : 1];
 #pragma unroll
   for (int t = 0; t < D / 16; ++t) {
     kf[t] = *(const bf16x8*)(k2r + 16 * t + 8 * half);
-    vf[t] = *(const bf16x8*)(v2r + 16 * t + 8 * half);
+    if constexpr (kDK) vf[t] = *(const bf16x8*)(v2r + 16 * t + 8 * half);
   }
-  floatx16 dk[D / 32], dv[D / 32];
+  floatx16 acc[D / 32];  // dK2^T or dV2^T
 #pragma unroll
-  for (int i = 0; i < D / 32; ++i) dk[i] = dv[i] = floatx16{};
+  for (int i = 0; i < D / 32; ++i) acc[i] = floatx16{};
 
   // step s <-> (t = tfirst + s / G, h = g*G + s % G)
   const int tfirst = k0;
@@ -804,42 +805,37 @@ __global__ __launch_bounds__(256, 1) void bwd_dkv2_mfma_kernel(BwdParams p, int 
     const char* At = tiles + (st & 1) * 2 * TILE;
     const char* Bt = At + TILE;
     const floatx16 sv = OPS::template rows_x<RS>(At, 0, lane, kf);  // C[j][key]
-    const floatx16 dp = OPS::template rows_x<RS>(Bt, 0, lane, vf);
-    uint32_t pp[8], pd[8];
+    floatx16 dp;
+    if constexpr (kDK) dp = OPS::template rows_x<RS>(Bt, 0, lane, vf);
+    uint32_t pk[8];  // bf16(dS) (dK2 launch) or bf16(P) (dV2 launch)
 #pragma unroll
     for (int e = 0; e < 16; e += 2) {
       const int i0 = 8 * (e >> 2) + 4 * half + (e & 3), i1 = i0 + 1;
       const bool ok0 = kok && i0 >= ilo, ok1 = kok && i1 >= ilo;
       const float p0 = ok0 ? fast_exp2(fmaf(sv[e], sl2s, -lse2)) : 0.f;
       const float p1 = ok1 ? fast_exp2(fmaf(sv[e + 1], sl2s, -lse2)) : 0.f;
-      pp[e >> 1] = pack_bf16(p0, p1);
-      pd[e >> 1] = pack_bf16(p0 * fmaf(dp[e], dpm, dsm), p1 * fmaf(dp[e + 1], dpm, dsm));
+      if constexpr (kDK) pk[e >> 1] = pack_bf16(p0 * fmaf(dp[e], dpm, dsm), p1 * fmaf(dp[e + 1], dpm, dsm));
+      else pk[e >> 1] = pack_bf16(p0, p1);
     }
-    const bf16x8 db0 = __builtin_bit_cast(bf16x8, u32x4{pd[0], pd[1], pd[2], pd[3]});
-    const bf16x8 db1 = __builtin_bit_cast(bf16x8, u32x4{pd[4], pd[5], pd[6], pd[7]});
-    OPS::template tr_acc<RS>(dk, At, 0, lane, db0, db1);  // dK2^T += A_t^T · dS^T
-    const bf16x8 pb0 = __builtin_bit_cast(bf16x8, u32x4{pp[0], pp[1], pp[2], pp[3]});
-    const bf16x8 pb1 = __builtin_bit_cast(bf16x8, u32x4{pp[4], pp[5], pp[6], pp[7]});
-    OPS::template tr_acc<RS>(dv, Bt, 0, lane, pb0, pb1);  // dV2^T += B_t^T · P^T
+    const bf16x8 b0 = __builtin_bit_cast(bf16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
+    const bf16x8 b1 = __builtin_bit_cast(bf16x8, u32x4{pk[4], pk[5], pk[6], pk[7]});
+    // dK2^T += A_t^T · dS^T, or dV2^T += B_t^T · P^T
+    OPS::template tr_acc<RS>(acc, kDK ? At : Bt, 0, lane, b0, b1);
   }
 
   // write: acc[db] holds d = 32*db + acc_row(r, half) of key kw
   if (kvalid) {
-    bf16* dkr = (bf16*)p.dk2 + (int64_t)kw * p.dk_st + (int64_t)g * p.dk_sh;
-    bf16* dvr = (bf16*)p.dv2 + (int64_t)kw * p.dv_st + (int64_t)g * p.dv_sh;
+    bf16* orow = kDK ? (bf16*)p.dk2 + (int64_t)kw * p.dk_st + (int64_t)g * p.dk_sh
+                     : (bf16*)p.dv2 + (int64_t)kw * p.dv_st + (int64_t)g * p.dv_sh;
 #pragma unroll
     for (int db = 0; db < D / 32; ++db)
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const int d = 32 * db + 8 * q4 + 4 * half;
-        bf16x4 a, b;
+        bf16x4 a;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          a[e] = (bf16)dk[db][4 * q4 + e];
-          b[e] = (bf16)dv[db][4 * q4 + e];
-        }
-        *(bf16x4*)(dkr + d) = a;
-        *(bf16x4*)(dvr + d) = b;
+        for (int e = 0; e < 4; ++e) a[e] = (bf16)acc[db][4 * q4 + e];
+        *(bf16x4*)(orow + d) = a;
       }
   }
 }
@@ -849,11 +845,14 @@ hipError_t launch_dkv2_d(const BwdParams& p, hipStream_t stream) {
   constexpr int RS = 2 * D + 32, RB = 2 * D;
   const size_t lds = (size_t)4 * 32 * RS + (size_t)kKvRing * 2 * RB + 3 * 1024;
   const int nblocks = (p.tokens + 127) / 128 * p.hk;
-  auto kern = bwd_dkv2_mfma_kernel<D>;
-  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3(nblocks), dim3(256), lds, stream, p, nblocks);
-  return hipGetLastError();
+  for (auto kern : {bwd_dkv2_mfma_kernel<D, 1>, bwd_dkv2_mfma_kernel<D, 2>}) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3(nblocks), dim3(256), lds, stream, p, nblocks);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 // bf16, DK == DV in {64, 128}, 16-byte aligned rows.
