@@ -173,6 +173,12 @@ def test_c2_full_size_sampled(cuda, seed):
     _check(cuda, 2, 4096, 16, 16, 128, 32, 512, torch.bfloat16, seed=seed, positions=pos, kernel="mfma")
 
 
+def test_ns_full_size_sampled(cuda):
+    """The north-star shape (C2 at S=8192: B2 H16 D128, 512x32, the bench workload), window-edge positions."""
+    pos = [0, 31, 32, 511, 512, 4095, 8191]
+    _check(cuda, 2, 8192, 16, 16, 128, 32, 512, torch.bfloat16, seed=0, positions=pos, kernel="mfma")
+
+
 def test_d256_config4_sampled_and_deterministic(cuda):
     """BASELINE config 4 shape family (D=256, w1=256, w2=64, sigma 0.5), shortened; bit-exact reruns."""
     attn, _, _ = _api()
