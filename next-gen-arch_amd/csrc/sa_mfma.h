@@ -421,10 +421,8 @@ struct RowBlock {
   template <int RSK, int RSV, bool NEXT>
   __device__ __forceinline__ void step(floatx16& s, float& cmax, const char* knext, const char* vtile, int row0,
                                        int lane, float sl2) {
-    static_assert(DK <= 128 && DV <= 128, "the pipelined step covers score and value widths up to 128");
     const int n = lane & 31, half = lane >> 5;
     constexpr int NT = DK / 16;   // QK^T MFMAs
-    constexpr int PER = 16 / NT; // probabilities per QK^T MFMA (2 or 4)
     floatx16 sn = floatx16{};
     uint32_t pk[8];              // P^T as packed bf16 pairs (B operand of the PV MFMAs)
     float zs = 0.f;
@@ -450,13 +448,15 @@ struct RowBlock {
         sn = mfma32x32x16(kf, a[t], sn);
       }
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int u = 0; u < PER; u += 2) {
-        const int r = t * PER + u;
-        const float p0 = fast_exp2(fmaf(s[r], sl2, -m)), p1 = fast_exp2(fmaf(s[r + 1], sl2, -m));
-        zs += p0 + p1;
-        pk[r >> 1] = pack_bf16(p0, p1);
-      }
+      // probability pair pi (scores 2pi, 2pi+1) goes with QK^T MFMA pi * NT / 8
+      static_for<0, 8>([&](auto pp) {
+        constexpr int pi = decltype(pp)::value;
+        if constexpr (pi * NT / 8 == t) {
+          const float p0 = fast_exp2(fmaf(s[2 * pi], sl2, -m)), p1 = fast_exp2(fmaf(s[2 * pi + 1], sl2, -m));
+          zs += p0 + p1;
+          pk[pi] = pack_bf16(p0, p1);
+        }
+      });
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (NEXT && t + 1 < NT) kf = kn;
     });
@@ -465,7 +465,6 @@ struct RowBlock {
     const bf16x8 pb1 = __builtin_bit_cast(bf16x8, u32x4{pk[4], pk[5], pk[6], pk[7]});
 
     // phase 2
-    constexpr int MPER = 16 / kSteps;  // score elements folded into the max per PV MFMA
     float rmax = -INFINITY;
     lds_wait(v1, v2);
     static_for<0, kSteps>([&](auto st) {
@@ -477,10 +476,11 @@ struct RowBlock {
       __builtin_amdgcn_sched_barrier(0);
       o[step % (DV / 32)] = mfma32x32x16(vf, step / (DV / 32) == 0 ? pb0 : pb1, o[step % (DV / 32)]);
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (NEXT) {
-#pragma unroll
-        for (int u = 0; u < MPER; u += 2)
-          rmax = fmaxf(rmax, fmaxf(sn[step * MPER + u], sn[step * MPER + u + 1]));
+      if constexpr (NEXT) {  // score v of the next chunk is folded in at PV MFMA v * kSteps / 16
+        static_for<0, 16>([&](auto vv2) {
+          constexpr int v = decltype(vv2)::value;
+          if constexpr (v * kSteps / 16 == step) rmax = fmaxf(rmax, sn[v]);
+        });
       }
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (step + 1 < kSteps) {

@@ -77,8 +77,10 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
   static_assert(!kSlot || NW * G::RSK <= G::kInstrV * 1024, "the q rows fit the short slot's V region");
   constexpr int R = P + 1;  // ring slots for the long-axis tiles
   constexpr int NI = G::NI;
-  // the pipelined loop holds a second score tile: registers allow it up to DK = DV = 128
-  constexpr bool kPipelined = DK <= 128 && DV <= 128 && P >= 2;
+  // the software-pipelined loop (a second score tile in flight) needs P >= 2:
+  // widths of 256 (one wave per SIMD, 512 registers); widths up to 128 run
+  // P = 1 at three waves per SIMD instead
+  constexpr bool kPipelined = P >= 2;
   extern __shared__ __attribute__((aligned(16))) char lds[];
   // kSlot: one more slot after the ring holds the short window of the pass:
   // its K region takes the k1 rows and (in its V region) the q rows of the NW
