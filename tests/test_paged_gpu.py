@@ -49,6 +49,35 @@ def test_matches_oracle_for_prefill_and_decode_tokens(cuda, dtype, tol, heads, k
     print(f"[{name}] {dtype} h{heads}/{kv_heads} w{short_window}x{long_window} hnd={hnd}", flush=True)
 
 
+@pytest.mark.parametrize("dim", [128, 256])
+@pytest.mark.parametrize("heads,kv_heads", [(4, 1), (4, 2), (4, 4)])
+def test_head_dims_128_and_256(cuda, dim, heads, kv_heads):
+    """bf16 MFMA paged kernels at the larger head dims (tasks of 1, 2 and 4 waves), prefill and decode tokens."""
+    paged, plan = _paged()
+    block_size, lengths, ws, wl = 16, [37, 90], 16, 48
+    (short, long), table, contiguous = paged_batch(lengths, kv_heads, dim, block_size, torch.bfloat16, seed=5,
+                                                   device=cuda)
+    g = torch.Generator().manual_seed(6)
+    seqs, positions, queries, expected = [], [], [], []
+    for s, (n, (k1, k2, v1, v2)) in enumerate(zip(lengths, contiguous)):
+        q = torch.randn(1, n, heads, dim, generator=g).to(torch.bfloat16)
+        oracle = O.reference_simplicial(q.double(), k1.double(), k2.double(), v1.double(), v2.double(), ws, wl)
+        for position in (range(n) if s == 0 else [n - 1]):
+            seqs.append(s)
+            positions.append(position)
+            queries.append(q[0, position])
+            expected.append(oracle[0, position])
+    q = torch.stack(queries).to(cuda)
+    seq = torch.tensor(seqs, dtype=torch.int32, device=cuda)
+    pos = torch.tensor(positions, dtype=torch.int32, device=cuda)
+    out = paged(q, short, long, table, seq, pos, short_window=ws, long_window=wl, scale=dim ** -0.5)
+    name = plan(q, short, long, table, seq, pos, short_window=ws, long_window=wl)[0]
+    err = (out.cpu() - torch.stack(expected).float()).abs().max().item()
+    print(f"[{name}] bf16 d{dim} h{heads}/{kv_heads}: max-abs {err:.2e}", flush=True)
+    assert name == "mfma"
+    torch.testing.assert_close(out.cpu(), torch.stack(expected).float(), rtol=3e-2, atol=3e-2)
+
+
 def test_token_order_and_batch_composition_do_not_change_results(cuda):
     paged, _ = _paged()
     dim, heads, kv_heads = 64, 4, 2
