@@ -74,12 +74,18 @@ struct TileGeom {
   __device__ static __forceinline__ char* dst(char* slot, int wid, int k) { return slot + (wid * NI + k) * 1024; }
 };
 
-// Tile geometry of the forward kernels: widths of 256 keep 32-byte pads on
-// both tiles (measured faster there with one wave per SIMD), smaller widths
-// the conflict-free pads.
+// Tile geometry of the forward kernels.  Widths of 256 keep 32-byte pads on
+// both tiles (measured faster there with one wave per SIMD).  Smaller widths
+// take the conflict-free 16-byte K pad; the V pad is 64 bytes (conflict-free
+// transposing reads) unless that costs each wave one more DMA instruction per
+// tile than a 32-byte pad (2-way conflicts on the V reads), as for the 35-row
+// tiles of 4-query blocks: there the fewer DMA instructions and registers
+// measured 3-4 % faster on NS and C2.
 template <int DK, int DV, int ROWS_T, int NW>
-using FwdGeom = std::conditional_t<(DK >= 256 || DV >= 256), TileGeom<DK, DV, ROWS_T, NW, 32, 32>,
-                                   TileGeom<DK, DV, ROWS_T, NW>>;
+using FwdGeom = std::conditional_t<
+    (DK >= 256 || DV >= 256), TileGeom<DK, DV, ROWS_T, NW, 32, 32>,
+    std::conditional_t<(TileGeom<DK, DV, ROWS_T, NW, 16, 64>::NI > TileGeom<DK, DV, ROWS_T, NW, 16, 32>::NI),
+                       TileGeom<DK, DV, ROWS_T, NW, 16, 32>, TileGeom<DK, DV, ROWS_T, NW, 16, 64>>>;
 
 // s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding:
 // vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
