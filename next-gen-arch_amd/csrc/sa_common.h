@@ -62,6 +62,21 @@ __device__ __forceinline__ int acc_row(int r, int half) { return 8 * (r >> 2) + 
 // the lane's own half, the other receives the opposite half).  Combining the
 // two registers therefore gives the same two-half result in all 64 lanes, in
 // the same operand order (bit-identical halves).
+// Lane index computed at the point of use.  The volatile asm can be neither
+// hoisted nor merged with an earlier lane index, so code after long loops
+// takes it from here instead of keeping the first one live (or spilled)
+// across the loops.
+__device__ __forceinline__ int fresh_lane() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
+// A wave-uniform float moved to a scalar register.
+__device__ __forceinline__ float uniform_f(float x) {
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
+}
+
 __device__ __forceinline__ float pair_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));

@@ -282,12 +282,13 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
     if constexpr (kSlot) wait_vmcnt<0>();  // this wave's part of the v1 rows
     block_barrier();  // ring reads done (LDS reused below); v1 rows complete
 
-    // ---- epilogue of this pass: merge the 32 rows of the wave
+    // ---- epilogue of this pass: merge the 32 rows of the wave.  The merge's
+    // max and sum are wave-uniform and held in scalar registers.
     const float zrow = pair_sum(rb.z);
     const float mrow = row_ok ? rb.m : -INFINITY;
-    const float Mw = wave_max(mrow);
+    const float Mw = uniform_f(wave_max(mrow));
     const float wgt = (row_ok && Mw > -INFINITY) ? fast_exp2(mrow - Mw) : 0.f;
-    const float Zw = half_sum(wgt * zrow);
+    const float Zw = uniform_f(half_sum(wgt * zrow));
     float* red = (float*)lds + wid * (64 * 36);  // [64 d][36] per wave (ring region)
     // this lane's v1 row
     const char* v1s = kSlot ? sslot + G::VOFF + srow * G::RSV : (const char*)(p.v1 + (int64_t)jc * v_st + v_g);
@@ -330,17 +331,21 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
       }
       orun[sl] = orun[sl] * a0 + acc * a1;
     }
-    Zrun = Zrun * a0 + Zw * a1;
-    Mrun = Mn;
+    Zrun = uniform_f(Zrun * a0 + Zw * a1);
+    Mrun = uniform_f(Mn);
     if (r + 1 < p.nr) block_barrier();  // every wave's `red` reads done before the next pass refills the ring
   }
 
   if (qvalid) {
+    // widths up to 128: the lane index for the stores is taken afresh rather
+    // than kept live through the key loop (measured faster; at widths of 256
+    // slower)
+    const int lf = kSlot ? lane : fresh_lane();
     const float inv = 1.f / Zrun;
     bf16* orow = p.out + (int64_t)t * p.o_st + (int64_t)h * p.o_sh;
 #pragma unroll
-    for (int i = 0; i < DV / 64; ++i) orow[64 * i + lane] = (bf16)(orun[i] * inv);
-    if (p.lse && lane == 0) p.lse[(int64_t)t * p.lse_st + h] = (Mrun + __log2f(Zrun)) * kLn2;
+    for (int i = 0; i < DV / 64; ++i) orow[64 * i + lf] = (bf16)(orun[i] * inv);
+    if (p.lse && lf == 0) p.lse[(int64_t)t * p.lse_st + h] = (Mrun + __log2f(Zrun)) * kLn2;
   }
 }
 
