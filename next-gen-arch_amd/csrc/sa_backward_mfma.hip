@@ -626,13 +626,14 @@ hipError_t launch_dkv1_d(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
 
 
 // ---------------------------------------------------------------------------
-// dk2, dv2: a workgroup of 4 waves owns 128 consecutive long keys of one KV
-// group; wave w's 32 keys are kw = k0 + 32w + lane % 32.  It walks the steps
-// (t, h) for t = k0 .. k0 + 127 + wl - 1 (every query whose long window can
-// reach a key of the block) and h over the group's heads.  Per step the waves
-// build A_t (rows j = t - 31 .. t: bf16(q_th ⊙ k1_j)) and B_t (bf16(dout_th ⊙
-// v1_j)) in LDS, 8 rows each; tiles are double-buffered, one barrier per
-// step.  Wave 0 stages each step's q, dout, k1_t and v1_t rows with one
+// dk2, dv2: a workgroup of NWK waves owns 32 * NWK consecutive long keys of
+// one KV group; wave w's 32 keys are kw = k0 + 32w + lane % 32.  It walks the
+// steps (t, h) for t = k0 .. k0 + 32 NWK - 1 + wl - 1 (every query whose long
+// window can reach a key of the block) and h over the group's heads.  Per
+// step the waves build A_t (rows j = t - 31 .. t: bf16(q_th ⊙ k1_j)) and B_t
+// (bf16(dout_th ⊙ v1_j)) in LDS, 32 / NWK rows each; tiles are
+// double-buffered, one barrier per step.  Wider blocks (NWK = 8 at D = 128)
+// share each step's tile formation, barrier and staging among more keys.  Wave 0 stages each step's q, dout, k1_t and v1_t rows with one
 // full-wave DMA two steps ahead; the k1 / v1 rows of earlier queries come
 // from a 64-row ring (row j at slot j % 64) into which wave 0 copies each
 // staged k1_t / v1_t.  Covers ws <= 32 (one 32-row block of short keys).
@@ -641,9 +642,11 @@ constexpr int kKvRing = 64;
 // MODE 1: dK2 only, MODE 2: dV2 only (two launches).  Each holds one
 // accumulator set, and the dV2 launch neither the V2 fragments nor dP, so
 // both fit two waves per SIMD; the S recomputation is paid twice.
-template <int D, int MODE>
-__global__ __launch_bounds__(256, 2) void bwd_dkv2_mfma_kernel(BwdParams p, int nblocks) {
+template <int D, int MODE, int NWK>
+__global__ __launch_bounds__(64 * NWK, 2) void bwd_dkv2_mfma_kernel(BwdParams p, int nblocks) {
   constexpr bool kDK = MODE == 1, kDV = MODE == 2;
+  constexpr int KB = 32 * NWK;    // keys per workgroup
+  constexpr int RPW = 32 / NWK;   // A / B rows formed per wave and step
   static_assert(kDK || kDV, "one output per launch");
   using OPS = BwdOps<D>;
   constexpr int RS = 2 * D + 32;           // A / B tile row stride (padded: row and transposing reads)
@@ -660,10 +663,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv2_mfma_kernel(BwdParams p, int 
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, n = lane & 31;
   const int lb = xcd_remap(blockIdx.x, nblocks);
-  const int kblocks = (p.tokens + 127) / 128;
+  const int kblocks = (p.tokens + KB - 1) / KB;
   const int kb = lb % kblocks;
   const int g = lb / kblocks;
-  const int k0 = kb * 128;
+  const int k0 = kb * KB;
   const int last = p.tokens - 1;
   const int kw = k0 + 32 * wid + n;  // this lane's key (column of the C layout)
   const int kwc = min(kw, last);
@@ -687,7 +690,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv2_mfma_kernel(BwdParams p, int 
 
   // step s <-> (t = tfirst + s / G, h = g*G + s % G)
   const int tfirst = k0;
-  const int tlast = min(last, k0 + 127 + p.wl - 1);
+  const int tlast = min(last, k0 + KB - 1 + p.wl - 1);
   const int nsteps = (tlast - tfirst + 1) * G;
 
   // Wave 0 stages step st: lane -> row (lane / kRowLanes) % 4, 16-byte segment
@@ -716,7 +719,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv2_mfma_kernel(BwdParams p, int 
   dma_step(0);
   dma_step(1);
   // the k1 / v1 rows before the first query (j = tfirst - 31 .. tfirst - 1) into the ring
-  for (int idx = tid; idx < 31 * 2 * kRowLanes; idx += 256) {
+  for (int idx = tid; idx < 31 * 2 * kRowLanes; idx += 64 * NWK) {
     const int jj = idx / (2 * kRowLanes), w = idx % (2 * kRowLanes);
     const int j = tfirst - 31 + jj;
     if (j >= 0) {
@@ -729,18 +732,20 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv2_mfma_kernel(BwdParams p, int 
   wait_vmcnt<0>();
   block_barrier();
 
-  // form A / B rows of step st into tile buffer b: wave w builds rows 8w .. 8w+7;
-  // row 31 (j = t) comes from the stage, earlier rows from the ring
+  // form A / B rows of step st into tile buffer b: wave w builds rows
+  // RPW w .. RPW w + RPW - 1; row 31 (j = t) comes from the stage, earlier rows
+  // from the ring
   auto form = [&](int st, int b) {
     const int t = tfirst + st / G;
     const char* sg_row = stage + (st % 3) * 1024;
     char* At = tiles + b * 2 * TILE;
     char* Bt = At + TILE;
     constexpr int SEGS = D / 8;  // 16-byte segments per row
+    static_assert(RPW * SEGS % 64 == 0, "whole lanes per formed row block");
 #pragma unroll
-    for (int u = 0; u < 8 * SEGS / 64; ++u) {
+    for (int u = 0; u < RPW * SEGS / 64; ++u) {
       const int idx = u * 64 + lane;
-      const int i = 8 * wid + idx / SEGS, sg = idx % SEGS;  // tile row, segment
+      const int i = RPW * wid + idx / SEGS, sg = idx % SEGS;  // tile row, segment
       const int j = max(t - 31 + i, 0);
       const char* kvrow = j == t ? sg_row + 2 * RB : ring + (j % kKvRing) * 2 * RB;
       const bf16x8 qv = *(const bf16x8*)(sg_row + 16 * sg);
@@ -802,6 +807,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv2_mfma_kernel(BwdParams p, int 
     // validity: key kw in [max(s0, t - wl + 1), t]; row i (j = t - 31 + i) in [max(s0, t - ws + 1), t]
     const bool kok = kvalid && kw <= t && kw >= max(s0, t - p.wl + 1);
     const int ilo = max(s0, t - p.ws + 1) - (t - 31);
+    // a wave none of whose 32 keys lies in t's long window skips the step
+    // (about a fifth of the steps at the block's ends)
+    const int kw0 = k0 + 32 * wid;
+    if (kw0 > t || kw0 + 31 < max(s0, t - p.wl + 1) || kw0 >= p.tokens) continue;
     const char* At = tiles + (st & 1) * 2 * TILE;
     const char* Bt = At + TILE;
     const floatx16 sv = OPS::template rows_x<RS>(At, 0, lane, kf);  // C[j][key]
@@ -843,12 +852,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dkv2_mfma_kernel(BwdParams p, int 
 template <int D>
 hipError_t launch_dkv2_d(const BwdParams& p, hipStream_t stream) {
   constexpr int RS = 2 * D + 32, RB = 2 * D;
+  constexpr int NWK = D >= 128 ? 8 : 4;  // one 8-wave workgroup per CU at D = 128, two 4-wave at 64
   const size_t lds = (size_t)4 * 32 * RS + (size_t)kKvRing * 2 * RB + 3 * 1024;
-  const int nblocks = (p.tokens + 127) / 128 * p.hk;
-  for (auto kern : {bwd_dkv2_mfma_kernel<D, 1>, bwd_dkv2_mfma_kernel<D, 2>}) {
+  const int nblocks = (p.tokens + 32 * NWK - 1) / (32 * NWK) * p.hk;
+  for (auto kern : {bwd_dkv2_mfma_kernel<D, 1, NWK>, bwd_dkv2_mfma_kernel<D, 2, NWK>}) {
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kern, dim3(nblocks), dim3(256), lds, stream, p, nblocks);
+    hipLaunchKernelGGL(kern, dim3(nblocks), dim3(64 * NWK), lds, stream, p, nblocks);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
