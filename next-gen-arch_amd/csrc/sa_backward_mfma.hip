@@ -41,11 +41,25 @@ struct BwdOps {
   // C = Tile · X^T over D: A operand = tile rows row0 .. row0+31 (row stride
   // RS bytes), B operand = the fragments x[D/16] (one 32-row block, k = d).
   // Lane (n, half) receives C[tile row 8*(r/4) + 4*half + r%4][x row n].
-  template <int RS>
+  // PF: fragments read that many MFMAs ahead (more LDS latency hidden per
+  // wave, 4 VGPRs each).
+  template <int RS, int PF = 1>
   __device__ static __forceinline__ floatx16 rows_x(const char* tile, int row0, int lane, const bf16x8* x) {
     const int n = lane & 31, half = lane >> 5;
     const char* kp = tile + (row0 + n) * RS + 16 * half;
     floatx16 c = floatx16{};
+    if constexpr (PF > 1) {
+      bf16x8 f[D / 16];
+      static_for<0, (PF < D / 16 ? PF : D / 16)>([&](auto s) { f[s] = *(const bf16x8*)(kp + 32 * s); });
+      static_for<0, D / 16>([&](auto st) {
+        constexpr int s = decltype(st)::value;
+        if constexpr (s + PF < D / 16) f[s + PF] = *(const bf16x8*)(kp + 32 * (s + PF));
+        __builtin_amdgcn_sched_barrier(0);
+        c = mfma32x32x16(f[s], x[s], c);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      return c;
+    }
     // fragments are read one step ahead of their MFMA; the scheduling barriers
     // keep the compiler from hoisting all D/16 reads (D/4 more live VGPRs)
     bf16x8 f = *(const bf16x8*)kp;
@@ -65,13 +79,31 @@ struct BwdOps {
   // transposed (d x rows, read with ds_read_b64_tr_b16), B operand = {pb0,
   // pb1}: the 32 x 32 values of a rows_x result (rows x columns) packed by
   // pack_c.  acc[db] holds d = 32*db + acc_row(r, half), column lane % 32.
-  template <int RS>
+  // PF: transposed reads issued that many MFMAs ahead.
+  template <int RS, int PF = 1>
   __device__ static __forceinline__ void tr_acc(floatx16* acc, const char* tile, int row0, int lane,
                                                 const bf16x8& pb0, const bf16x8& pb1) {
     const int half = lane >> 5, g16 = (lane >> 4) & 1, i16 = lane & 15;
     const int e_src = i16 >> 2, q_src = i16 & 3;
     const uint32_t vp = lds_addr(tile + (row0 + 4 * half + e_src) * RS + 32 * g16 + 8 * q_src);
     constexpr int kSteps = 2 * (D / 32);
+    if constexpr (PF > 1) {
+      shortx4 va[kSteps], vb[kSteps];
+      static_for<0, (PF < kSteps ? PF : kSteps)>([&](auto s) { RB::template vread<RS, s>(vp, va[s], vb[s]); });
+      static_for<0, kSteps>([&](auto st) {
+        constexpr int s = decltype(st)::value;
+        if constexpr (s + PF < kSteps) RB::template vread<RS, s + PF>(vp, va[s + PF], vb[s + PF]);
+        // reads issued after step s's: 2 per later step in flight
+        constexpr int later = (s + PF < kSteps ? s + PF : kSteps - 1) - s;
+        lds_wait_n<2 * later>(va[s], vb[s]);
+        shortx8 vv = {va[s][0], va[s][1], va[s][2], va[s][3], vb[s][0], vb[s][1], vb[s][2], vb[s][3]};
+        const bf16x8 vf = __builtin_bit_cast(bf16x8, vv);
+        __builtin_amdgcn_sched_barrier(0);
+        acc[s % (D / 32)] = mfma32x32x16(vf, s / (D / 32) == 0 ? pb0 : pb1, acc[s % (D / 32)]);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      return;
+    }
     shortx4 v1, v2;
     RB::template vread<RS, 0>(vp, v1, v2);
     lds_wait(v1, v2);
@@ -514,7 +546,9 @@ __global__ __launch_bounds__(64 * NQ * NH, 2) void bwd_dkv1_mfma_kernel(BwdParam
         const int klo = max(max(s0 - kfirst, n - kChunk * c), 0);
         const int khi = min(n + p.wl - 1 - kChunk * c, kChunk - 1);
         const char* slot = lds + (c % R) * G::SLOT;
-        const floatx16 sv = OPS::template rows_x<G::RSK>(slot, qo, lane, ra.a);
+        // dv1 launch (registers to spare): reads two MFMAs ahead
+        constexpr int kPF = kDV ? 2 : 1;
+        const floatx16 sv = OPS::template rows_x<G::RSK, kPF>(slot, qo, lane, ra.a);
         floatx16 dp;
         if constexpr (kDK) dp = OPS::template rows_x<G::RSV>(slot + G::VOFF, qo, lane, rbv.a);
         const int lo_h = klo - 4 * half, hi_h = khi - 4 * half;
@@ -535,7 +569,7 @@ __global__ __launch_bounds__(64 * NQ * NH, 2) void bwd_dkv1_mfma_kernel(BwdParam
         const bf16x8 b0 = __builtin_bit_cast(bf16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
         const bf16x8 b1 = __builtin_bit_cast(bf16x8, u32x4{pk[4], pk[5], pk[6], pk[7]});
         if constexpr (kDK) OPS::template tr_acc<G::RSK>(acc, slot, qo, lane, b0, b1);  // G^T += K2^T · dS^T
-        else OPS::template tr_acc<G::RSV>(acc, slot + G::VOFF, qo, lane, b0, b1);      // O''^T += V2^T · P^T
+        else OPS::template tr_acc<G::RSV, kPF>(acc, slot + G::VOFF, qo, lane, b0, b1);  // O''^T += V2^T · P^T
       }
       wait_vmcnt<0>();
       block_barrier();  // ring reads done (LDS reused below)
@@ -638,6 +672,9 @@ hipError_t launch_dkv1_d(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
 // from a 64-row ring (row j at slot j % 64) into which wave 0 copies each
 // staged k1_t / v1_t.  Covers ws <= 32 (one 32-row block of short keys).
 constexpr int kKvRing = 64;
+#ifndef SA_DKV2_PF
+#define SA_DKV2_PF 2
+#endif
 
 // MODE 1: dK2 only, MODE 2: dV2 only (two launches).  Each holds one
 // accumulator set, and the dV2 launch neither the V2 fragments nor dP, so
@@ -647,6 +684,9 @@ __global__ __launch_bounds__(64 * NWK, 2) void bwd_dkv2_mfma_kernel(BwdParams p,
   constexpr bool kDK = MODE == 1, kDV = MODE == 2;
   constexpr int KB = 32 * NWK;    // keys per workgroup
   constexpr int RPW = 32 / NWK;   // A / B rows formed per wave and step
+  // LDS reads in flight ahead of their MFMA: with two waves per SIMD, one
+  // read ahead leaves each step's three MFMA chains waiting on LDS latency
+  constexpr int kPF = SA_DKV2_PF;
   static_assert(kDK || kDV, "one output per launch");
   using OPS = BwdOps<D>;
   constexpr int RS = 2 * D + 32;           // A / B tile row stride (padded: row and transposing reads)
@@ -813,9 +853,9 @@ __global__ __launch_bounds__(64 * NWK, 2) void bwd_dkv2_mfma_kernel(BwdParams p,
     if (kw0 > t || kw0 + 31 < max(s0, t - p.wl + 1) || kw0 >= p.tokens) continue;
     const char* At = tiles + (st & 1) * 2 * TILE;
     const char* Bt = At + TILE;
-    const floatx16 sv = OPS::template rows_x<RS>(At, 0, lane, kf);  // C[j][key]
+    const floatx16 sv = OPS::template rows_x<RS, kPF>(At, 0, lane, kf);  // C[j][key]
     floatx16 dp;
-    if constexpr (kDK) dp = OPS::template rows_x<RS>(Bt, 0, lane, vf);
+    if constexpr (kDK) dp = OPS::template rows_x<RS, kPF>(Bt, 0, lane, vf);
     uint32_t pk[8];  // bf16(dS) (dK2 launch) or bf16(P) (dV2 launch)
 #pragma unroll
     for (int e = 0; e < 16; e += 2) {
@@ -829,7 +869,7 @@ __global__ __launch_bounds__(64 * NWK, 2) void bwd_dkv2_mfma_kernel(BwdParams p,
     const bf16x8 b0 = __builtin_bit_cast(bf16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
     const bf16x8 b1 = __builtin_bit_cast(bf16x8, u32x4{pk[4], pk[5], pk[6], pk[7]});
     // dK2^T += A_t^T · dS^T, or dV2^T += B_t^T · P^T
-    OPS::template tr_acc<RS>(acc, kDK ? At : Bt, 0, lane, b0, b1);
+    OPS::template tr_acc<RS, kPF>(acc, kDK ? At : Bt, 0, lane, b0, b1);
   }
 
   // write: acc[db] holds d = 32*db + acc_row(r, half) of key kw

@@ -164,6 +164,15 @@ __device__ __forceinline__ void lds_wait(shortx4& a, shortx4& b) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b));
 }
 
+// Wait until at most N of this wave's LDS operations are outstanding.  LDS
+// operations complete in order, so with N issued after the reads that fill a
+// and b, those reads are done (SMEM loads in flight only make it stricter).
+template <int N>
+__device__ __forceinline__ void lds_wait_n(shortx4& a, shortx4& b) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt is 4 bits");
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
+}
+
 // Initial running max: finite, so that exp2(s*c - m) of a masked score
 // (s = -inf) is exactly 0 even before a row has seen a valid key; the first
 // valid chunk always triggers a rescale (by exp2(kMInit - m') = 0).
