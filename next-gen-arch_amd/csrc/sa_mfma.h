@@ -433,7 +433,9 @@ struct RowBlock {
   // the rescale for chunk c has been applied.  With NEXT, the QK^T of chunk
   // c+1 (K tile `knext`) is computed into `s` and its scaled row max into
   // `cmax`.  `vtile` is chunk c's V tile; both tiles use rows row0.. .
-  template <int RSK, int RSV, bool NEXT>
+  // PF: V fragments read that many PV MFMAs ahead (the first PF issued before
+  // phase 1); 1 waits for each read right after the MFMA before it.
+  template <int RSK, int RSV, bool NEXT, int PF = 1>
   __device__ __forceinline__ void step(floatx16& s, float& cmax, const char* knext, const char* vtile, int row0,
                                        int lane, float sl2) {
     const int n = lane & 31, half = lane >> 5;
@@ -447,8 +449,10 @@ struct RowBlock {
     const int e_src = i16 >> 2, q_src = i16 & 3;
     const uint32_t vp = lds_addr(vtile + (row0 + 4 * half + e_src) * RSV + 32 * g16 + 8 * q_src);
     constexpr int kSteps = 2 * (DV / 32);
-    shortx4 v1, v2;
-    vread<RSV, 0>(vp, v1, v2);
+    constexpr int kPre = PF < kSteps ? PF : kSteps;
+    shortx4 v1, v2, va[kSteps], vb[kSteps];
+    if constexpr (PF > 1) static_for<0, kPre>([&](auto q) { vread<RSV, decltype(q)::value>(vp, va[q], vb[q]); });
+    else vread<RSV, 0>(vp, v1, v2);
 
     // phase 1
     const char* kp = knext + (row0 + n) * RSK + 16 * half;
@@ -481,6 +485,32 @@ struct RowBlock {
 
     // phase 2
     float rmax = -INFINITY;
+    if constexpr (PF > 1) {
+      static_for<0, kSteps>([&](auto st) {
+        constexpr int step = decltype(st)::value;
+        if constexpr (step + PF < kSteps) vread<RSV, step + PF>(vp, va[step + PF], vb[step + PF]);
+        constexpr int later = (step + PF < kSteps ? step + PF : kSteps - 1) - step;  // read pairs issued after
+        lds_wait_n<2 * later>(va[step], vb[step]);
+        shortx8 vv = {va[step][0], va[step][1], va[step][2], va[step][3],
+                      vb[step][0], vb[step][1], vb[step][2], vb[step][3]};
+        const bf16x8 vf = __builtin_bit_cast(bf16x8, vv);
+        __builtin_amdgcn_sched_barrier(0);
+        o[step % (DV / 32)] = mfma32x32x16(vf, step / (DV / 32) == 0 ? pb0 : pb1, o[step % (DV / 32)]);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (NEXT) {
+          static_for<0, 16>([&](auto vv2) {
+            constexpr int v = decltype(vv2)::value;
+            if constexpr (v * kSteps / 16 == step) rmax = fmaxf(rmax, sn[v]);
+          });
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      if constexpr (NEXT) {
+        cmax = pair_max(rmax) * sl2;
+        s = sn;
+      }
+      return;
+    }
     lds_wait(v1, v2);
     static_for<0, kSteps>([&](auto st) {
       constexpr int step = decltype(st)::value;

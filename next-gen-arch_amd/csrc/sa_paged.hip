@@ -55,13 +55,17 @@ struct PagedParams {
   float* lse;
 };
 
-constexpr int kPosCache = 1024;  // long-window positions of one split whose row offsets are kept in LDS
+constexpr int kPosCache = 1024;
+#ifndef SA_PAGED_STEP_PF
+#define SA_PAGED_STEP_PF 1
+#endif  // long-window positions of one split whose row offsets are kept in LDS
 
 template <int D, int NW, int P>
 __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel(PagedParams p) {
   using G = FwdGeom<D, D, kChunk, NW>;
   using RB = RowBlock<D, D>;
   constexpr bool kPipelined = D <= 128 && P >= 2;  // second score tile fits the registers up to D = 128
+  constexpr int kStepPF = SA_PAGED_STEP_PF;  // V fragments read ahead of the PV MFMAs (2 and 3 measured no faster)
   constexpr int SLOT = G::SLOT;
   constexpr int R = P + 1;
   constexpr int NI = G::NI;  // DMA instructions per wave per tile
@@ -225,11 +229,12 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
         wait_tiles<NI, P>(min(P - 2, cend - 2 - c));
         begin_chunk(c);
         const char* slot = lds + (c % R) * SLOT;
-        rb.template step<G::RSK, G::RSV, true>(s, cmax, lds + ((c + 1) % R) * SLOT, slot + G::VOFF, 0, lane, p.sl2);
+        rb.template step<G::RSK, G::RSV, true, kStepPF>(s, cmax, lds + ((c + 1) % R) * SLOT, slot + G::VOFF, 0, lane,
+                                                        p.sl2);
       }
       begin_chunk(c);
       const char* slot = lds + (c % R) * SLOT;
-      rb.template step<G::RSK, G::RSV, false>(s, cmax, slot, slot + G::VOFF, 0, lane, p.sl2);
+      rb.template step<G::RSK, G::RSV, false, kStepPF>(s, cmax, slot, slot + G::VOFF, 0, lane, p.sl2);
     } else {
       for (int c = cbeg; c < cend; ++c) {
         wait_tiles<NI, P>(min(P - 1, cend - 1 - c));

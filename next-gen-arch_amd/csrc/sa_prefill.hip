@@ -63,6 +63,9 @@ struct PrefillParams {
 #ifndef SA_PREFILL_DEPTH
 #define SA_PREFILL_DEPTH 1
 #endif
+#ifndef SA_PREFILL_STEP_PF
+#define SA_PREFILL_STEP_PF 2
+#endif
 
 template <int DK, int DV, int NQ, int NH, int P>
 __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREFILL_WAVES_PER_SIMD)) void prefill_mfma_kernel(
@@ -81,6 +84,7 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
   // widths of 256 (one wave per SIMD, 512 registers); widths up to 128 run
   // P = 1 at three waves per SIMD instead
   constexpr bool kPipelined = P >= 2;
+  constexpr int kStepPF = SA_PREFILL_STEP_PF;  // V fragments read ahead of the pipelined PV MFMAs (one wave per SIMD)
   extern __shared__ __attribute__((aligned(16))) char lds[];
   // kSlot: one more slot after the ring holds the short window of the pass:
   // its K region takes the k1 rows and (in its V region) the q rows of the NW
@@ -248,13 +252,13 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
           wait_tiles<NI, P>(min(P - 2, p.nc - 2 - c));
           begin_chunk(c, s, cmax);
           const char* slot = lds + (c % R) * G::SLOT;
-          rb.template step<G::RSK, G::RSV, true>(s, cmax, lds + ((c + 1) % R) * G::SLOT, slot + G::VOFF, qo, lane,
+          rb.template step<G::RSK, G::RSV, true, kStepPF>(s, cmax, lds + ((c + 1) % R) * G::SLOT, slot + G::VOFF, qo, lane,
                                                  p.sl2);
         }
         begin_chunk(c, s, cmax);
         if constexpr (kSlot) dma_tile(std::integral_constant<int, 2>{}, sslot, kbs, p.k1, p.v1);  // v1 rows
         const char* slot = lds + (c % R) * G::SLOT;
-        rb.template step<G::RSK, G::RSV, false>(s, cmax, slot, slot + G::VOFF, qo, lane, p.sl2);
+        rb.template step<G::RSK, G::RSV, false, kStepPF>(s, cmax, slot, slot + G::VOFF, qo, lane, p.sl2);
       } else if constexpr (kSlot) {
         dma_tile(std::integral_constant<int, 2>{}, sslot, kbs, p.k1, p.v1);
       }
