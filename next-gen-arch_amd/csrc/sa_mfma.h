@@ -277,7 +277,9 @@ struct RowBlock {
   // stride RSK bytes) and the V tile at `vtile` (row stride RSV).  sl2 = |scale|*log2(e) >= 0.
   // key_lo/key_hi: range of valid chunk keys (0..31) for this wave's query;
   // masking is applied only when the chunk is not fully valid.
-  template <int RSK, int RSV>
+  // PF: V fragments read that many PV MFMAs ahead (1: each read is waited
+  // for right after the MFMA before it).
+  template <int RSK, int RSV, int PF = 1>
   __device__ __forceinline__ void chunk(const char* ktile, const char* vtile, int row0, int lane, float sl2,
                                         int key_lo, int key_hi) {
     const int n = lane & 31, half = lane >> 5;
@@ -355,8 +357,25 @@ struct RowBlock {
     const int g16 = (lane >> 4) & 1, i16 = lane & 15;
     const int e_src = i16 >> 2, q_src = i16 & 3;
     const uint32_t vp = lds_addr(vtile + (row0 + 4 * half + e_src) * RSV + 32 * g16 + 8 * q_src);
-    // V fragments are read one step ahead of their MFMA
     constexpr int kSteps = 2 * (DV / 32);
+    if constexpr (PF > 1) {
+      shortx4 va[kSteps], vb[kSteps];
+      static_for<0, (PF < kSteps ? PF : kSteps)>([&](auto q) { vread<RSV, decltype(q)::value>(vp, va[q], vb[q]); });
+      static_for<0, kSteps>([&](auto st) {
+        constexpr int step = decltype(st)::value;
+        if constexpr (step + PF < kSteps) vread<RSV, step + PF>(vp, va[step + PF], vb[step + PF]);
+        constexpr int later = (step + PF < kSteps ? step + PF : kSteps - 1) - step;  // read pairs issued after
+        lds_wait_n<2 * later>(va[step], vb[step]);
+        shortx8 vv = {va[step][0], va[step][1], va[step][2], va[step][3],
+                      vb[step][0], vb[step][1], vb[step][2], vb[step][3]};
+        const bf16x8 vf = __builtin_bit_cast(bf16x8, vv);
+        __builtin_amdgcn_sched_barrier(0);
+        o[step % (DV / 32)] = mfma32x32x16(vf, pb[step / (DV / 32)], o[step % (DV / 32)]);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      return;
+    }
+    // V fragments are read one step ahead of their MFMA
     shortx4 v1, v2;
     vread<RSV, 0>(vp, v1, v2);
     lds_wait(v1, v2);

@@ -63,6 +63,11 @@ struct PrefillParams {
 #ifndef SA_PREFILL_DEPTH
 #define SA_PREFILL_DEPTH 1
 #endif
+// V fragments read ahead of the PV MFMAs in the chunk loop (widths <= 128);
+// reading K fragments further ahead than one spills in the loop
+#ifndef SA_PREFILL_CHUNK_PF
+#define SA_PREFILL_CHUNK_PF 3
+#endif
 #ifndef SA_PREFILL_STEP_PF
 #define SA_PREFILL_STEP_PF 2
 #endif
@@ -276,7 +281,7 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
         const bool active = qvalid && c >= cfirst;
         const int kfirst = t - p.wl + 1 + kChunk * c;  // key of this wave's chunk row 0
         const char* slot = lds + (c % R) * G::SLOT;
-        rb.template chunk<G::RSK, G::RSV>(slot, slot + G::VOFF, qo, lane, p.sl2,
+        rb.template chunk<G::RSK, G::RSV, SA_PREFILL_CHUNK_PF>(slot, slot + G::VOFF, qo, lane, p.sl2,
                                           active ? max(lo2 - kfirst, 0) : kChunk,
                                           active ? min(t - kfirst, kChunk - 1) : -1);
       }
