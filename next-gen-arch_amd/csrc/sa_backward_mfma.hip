@@ -33,6 +33,17 @@ namespace sa {
 
 namespace {
 
+// LDS fragments read ahead of their MFMA in each pass (see BwdOps)
+#ifndef SA_DQ_PF
+#define SA_DQ_PF 1
+#endif
+#ifndef SA_DK1_PF
+#define SA_DK1_PF 1
+#endif
+#ifndef SA_DKV2_PF
+#define SA_DKV2_PF 2
+#endif
+
 // Wave-level tile products used by the backward passes (D = head dim).
 template <int D>
 struct BwdOps {
@@ -289,8 +300,8 @@ __global__ __launch_bounds__(64 * NQ * NH, 2) void bwd_dq_mfma_kernel(BwdParams 
       const int klo = active ? max(lo2 - kfirst, 0) : kChunk;
       const int khi = active ? min(t - kfirst, kChunk - 1) : -1;
       const char* slot = lds + (c % R) * G::SLOT;
-      const floatx16 s = OPS::template rows_x<G::RSK>(slot, qo, lane, ra.a);
-      const floatx16 dp = OPS::template rows_x<G::RSV>(slot + G::VOFF, qo, lane, rbv.a);
+      const floatx16 s = OPS::template rows_x<G::RSK, SA_DQ_PF>(slot, qo, lane, ra.a);
+      const floatx16 dp = OPS::template rows_x<G::RSV, SA_DQ_PF>(slot + G::VOFF, qo, lane, rbv.a);
       // register r holds chunk key 8*(r/4) + r%4 + 4*half of column j = this lane's row
       const int lo_h = klo - 4 * half, hi_h = khi - 4 * half;
       float ds[16];
@@ -303,7 +314,7 @@ __global__ __launch_bounds__(64 * NQ * NH, 2) void bwd_dq_mfma_kernel(BwdParams 
       }
       bf16x8 pb0, pb1;
       OPS::pack_c(ds, pb0, pb1);
-      OPS::template tr_acc<G::RSK>(dA, slot, qo, lane, pb0, pb1);  // dA^T += K2^T · dS^T
+      OPS::template tr_acc<G::RSK, SA_DQ_PF>(dA, slot, qo, lane, pb0, pb1);  // dA^T += K2^T · dS^T
     }
     wait_vmcnt<0>();
     block_barrier();  // ring reads done (LDS reused below)
@@ -547,7 +558,7 @@ __global__ __launch_bounds__(64 * NQ * NH, 2) void bwd_dkv1_mfma_kernel(BwdParam
         const int khi = min(n + p.wl - 1 - kChunk * c, kChunk - 1);
         const char* slot = lds + (c % R) * G::SLOT;
         // dv1 launch (registers to spare): reads two MFMAs ahead
-        constexpr int kPF = kDV ? 2 : 1;
+        constexpr int kPF = kDV ? 2 : SA_DK1_PF;
         const floatx16 sv = OPS::template rows_x<G::RSK, kPF>(slot, qo, lane, ra.a);
         floatx16 dp;
         if constexpr (kDK) dp = OPS::template rows_x<G::RSV>(slot + G::VOFF, qo, lane, rbv.a);
@@ -672,9 +683,6 @@ hipError_t launch_dkv1_d(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
 // from a 64-row ring (row j at slot j % 64) into which wave 0 copies each
 // staged k1_t / v1_t.  Covers ws <= 32 (one 32-row block of short keys).
 constexpr int kKvRing = 64;
-#ifndef SA_DKV2_PF
-#define SA_DKV2_PF 2
-#endif
 
 // MODE 1: dK2 only, MODE 2: dV2 only (two launches).  Each holds one
 // accumulator set, and the dV2 launch neither the V2 fragments nor dP, so
