@@ -19,8 +19,10 @@
 // Score and value widths up to 128: the ring (P = 1) is the only LDS the
 // workgroup holds, so three workgroups share a CU (three waves per SIMD hide
 // each other's barrier and load latencies); the A rows and the epilogue's v1
-// rows are read from global memory.  Widths of 256 run one wave per SIMD and
-// stage the short window in one more LDS slot instead.
+// rows are read from global memory.  Widths of 256 stage the short window in
+// one more LDS slot and split each (token, head)'s value columns over two
+// waves: eight waves per workgroup, one workgroup and two waves per SIMD with
+// 256 registers each (both waves compute the score tile, each half of O).
 //
 // The joint softmax is kept per A row (running max / sum); the epilogue merges
 // the rows with their log-sum-exp weights and applies v1:
@@ -68,16 +70,24 @@ struct PrefillParams {
 #ifndef SA_PREFILL_CHUNK_PF
 #define SA_PREFILL_CHUNK_PF 3
 #endif
+#ifndef SA_PREFILL_WIDE_VS
+#define SA_PREFILL_WIDE_VS 2  // value split at widths of 256
+#endif
 #ifndef SA_PREFILL_STEP_PF
 #define SA_PREFILL_STEP_PF 2
 #endif
 
-template <int DK, int DV, int NQ, int NH, int P>
-__global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREFILL_WAVES_PER_SIMD)) void prefill_mfma_kernel(
-    PrefillParams p) {
-  static_assert(NQ * NH == 4, "4 waves per block");
+// VS: waves per (token, head) that split the value width (each computes the
+// full score tile and DV / VS output columns).  VS = 2 at widths of 256 gives
+// two waves per SIMD (256 registers each) instead of one with 512.
+template <int DK, int DV, int NQ, int NH, int P, int VS>
+__global__ __launch_bounds__(64 * NQ * NH * VS, (DK >= 256 || DV >= 256 ? VS : SA_PREFILL_WAVES_PER_SIMD)) void
+prefill_mfma_kernel(PrefillParams p) {
+  static_assert(NQ * NH == 4, "4 (token, head) pairs per block");
   static_assert(P >= 1 && P <= 4, "prefetch depth");
-  constexpr int NW = NQ * NH;
+  static_assert(VS == 1 || VS == 2, "value split");
+  constexpr int NW = NQ * NH * VS;
+  constexpr int DVW = DV / VS;  // value columns of one wave
   constexpr int ROWS = kChunk + NQ - 1;  // tile rows: one chunk of all NQ queries
   using G = FwdGeom<DK, DV, ROWS, NW>;
   // short window staged in an LDS slot (widths of 256) or read from global memory
@@ -86,10 +96,10 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
   constexpr int R = P + 1;  // ring slots for the long-axis tiles
   constexpr int NI = G::NI;
   // the software-pipelined loop (a second score tile in flight) needs P >= 2:
-  // widths of 256 (one wave per SIMD, 512 registers); widths up to 128 run
+  // widths of 256 (two value-split waves per SIMD); widths up to 128 run
   // P = 1 at three waves per SIMD instead
   constexpr bool kPipelined = P >= 2;
-  constexpr int kStepPF = SA_PREFILL_STEP_PF;  // V fragments read ahead of the pipelined PV MFMAs (one wave per SIMD)
+  constexpr int kStepPF = SA_PREFILL_STEP_PF;  // V fragments read ahead of the pipelined PV MFMAs
   extern __shared__ __attribute__((aligned(16))) char lds[];
   // kSlot: one more slot after the ring holds the short window of the pass:
   // its K region takes the k1 rows and (in its V region) the q rows of the NW
@@ -102,7 +112,9 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
   // wave index as a uniform (scalar) value: everything derived from it stays
   // in SGPRs and the control flow below stays scalar
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int hw = wid % NH, qo = wid / NH;
+  const int vs = VS == 1 ? 0 : wid % VS;  // this wave's value-column half
+  const int wq = wid / VS;                // (token, head) index in the block
+  const int hw = wq % NH, qo = wq / NH;
 
   const int lb = xcd_remap(blockIdx.x, p.nblocks);
   const int qb = lb % p.qblocks;
@@ -188,21 +200,22 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
         const int b = k * 1024 + lane * 16;
         int row = b / G::RSK, seg = (b % G::RSK) >> 4;
         if (row >= NW || seg >= G::kSegsK) row = 0, seg = 0;
-        const int tq = min(t0 + row / NH, last);
-        const int hq = g * p.group + hs * NH + row % NH;
+        const int tq = min(t0 + row / VS / NH, last);
+        const int hq = g * p.group + hs * NH + row / VS % NH;
         dma16(p.q + (int64_t)tq * p.q_st + (int64_t)hq * p.q_sh + seg * 8, sslot + G::VOFF + k * 1024);
       }
     }
   };
 
   const int half = lane >> 5, n = lane & 31;
-  using RB = RowBlock<DK, DV>;
+  using RB = RowBlock<DK, DVW>;
   RB rb;
-  // Running merge over the row-group passes: out values for d = 64*i + lane,
-  // plus (M, Z) in the log2 domain.
-  float orun[DV / 64];
+  const int vcol = vs * DVW * 2;  // byte offset of this wave's value columns in a V row
+  // Running merge over the row-group passes: out values for d = 64*i + lane
+  // (of this wave's columns), plus (M, Z) in the log2 domain.
+  float orun[DVW / 64];
 #pragma unroll
-  for (int i = 0; i < DV / 64; ++i) orun[i] = 0.f;
+  for (int i = 0; i < DVW / 64; ++i) orun[i] = 0.f;
   float Mrun = -INFINITY, Zrun = 0.f;
 
   for (int r = 0; r < p.nr; ++r) {
@@ -257,13 +270,13 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
           wait_tiles<NI, P>(min(P - 2, p.nc - 2 - c));
           begin_chunk(c, s, cmax);
           const char* slot = lds + (c % R) * G::SLOT;
-          rb.template step<G::RSK, G::RSV, true, kStepPF>(s, cmax, lds + ((c + 1) % R) * G::SLOT, slot + G::VOFF, qo, lane,
-                                                 p.sl2);
+          rb.template step<G::RSK, G::RSV, true, kStepPF>(s, cmax, lds + ((c + 1) % R) * G::SLOT,
+                                                          slot + G::VOFF + vcol, qo, lane, p.sl2);
         }
         begin_chunk(c, s, cmax);
         if constexpr (kSlot) dma_tile(std::integral_constant<int, 2>{}, sslot, kbs, p.k1, p.v1);  // v1 rows
         const char* slot = lds + (c % R) * G::SLOT;
-        rb.template step<G::RSK, G::RSV, false, kStepPF>(s, cmax, slot, slot + G::VOFF, qo, lane, p.sl2);
+        rb.template step<G::RSK, G::RSV, false, kStepPF>(s, cmax, slot, slot + G::VOFF + vcol, qo, lane, p.sl2);
       } else if constexpr (kSlot) {
         dma_tile(std::integral_constant<int, 2>{}, sslot, kbs, p.k1, p.v1);
       }
@@ -281,7 +294,7 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
         const bool active = qvalid && c >= cfirst;
         const int kfirst = t - p.wl + 1 + kChunk * c;  // key of this wave's chunk row 0
         const char* slot = lds + (c % R) * G::SLOT;
-        rb.template chunk<G::RSK, G::RSV, SA_PREFILL_CHUNK_PF>(slot, slot + G::VOFF, qo, lane, p.sl2,
+        rb.template chunk<G::RSK, G::RSV, SA_PREFILL_CHUNK_PF>(slot, slot + G::VOFF + vcol, qo, lane, p.sl2,
                                           active ? max(lo2 - kfirst, 0) : kChunk,
                                           active ? min(t - kfirst, kChunk - 1) : -1);
       }
@@ -300,22 +313,22 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
     const float Zw = uniform_f(half_sum(wgt * zrow));
     float* red = (float*)lds + wid * (64 * 36);  // [64 d][36] per wave (ring region)
     // this lane's v1 row
-    const char* v1s = kSlot ? sslot + G::VOFF + srow * G::RSV : (const char*)(p.v1 + (int64_t)jc * v_st + v_g);
+    const char* v1s = (kSlot ? sslot + G::VOFF + srow * G::RSV : (const char*)(p.v1 + (int64_t)jc * v_st + v_g)) + vcol;
     const float Mn = fmaxf(Mrun, Mw);
     const float a0 = Mrun > -INFINITY ? fast_exp2(Mrun - Mn) : 0.f;
     const float a1 = Mw > -INFINITY ? fast_exp2(Mw - Mn) : 0.f;
     // every v1 read is issued before the first use (one LDS wait, not one per
     // read); rows outside the window are zeroed by a select after the load
-    bf16x4 v1v[DV / 64][2][4];
+    bf16x4 v1v[DVW / 64][2][4];
 #pragma unroll
-    for (int sl = 0; sl < DV / 64; ++sl)
+    for (int sl = 0; sl < DVW / 64; ++sl)
 #pragma unroll
       for (int dbl = 0; dbl < 2; ++dbl)
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4)
           v1v[sl][dbl][q4] = *(const bf16x4*)(v1s + 2 * (64 * sl + 32 * dbl + 8 * q4 + 4 * half));
 #pragma unroll
-    for (int sl = 0; sl < DV / 64; ++sl) {
+    for (int sl = 0; sl < DVW / 64; ++sl) {
 #pragma unroll
       for (int dbl = 0; dbl < 2; ++dbl) {
         const int db = 2 * sl + dbl;
@@ -351,10 +364,10 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 1 : SA_PREF
     // slower)
     const int lf = kSlot ? lane : fresh_lane();
     const float inv = 1.f / Zrun;
-    bf16* orow = p.out + (int64_t)t * p.o_st + (int64_t)h * p.o_sh;
+    bf16* orow = p.out + (int64_t)t * p.o_st + (int64_t)h * p.o_sh + vs * DVW;
 #pragma unroll
-    for (int i = 0; i < DV / 64; ++i) orow[64 * i + lf] = (bf16)(orun[i] * inv);
-    if (p.lse && lf == 0) p.lse[(int64_t)t * p.lse_st + h] = (Mrun + __log2f(Zrun)) * kLn2;
+    for (int i = 0; i < DVW / 64; ++i) orow[64 * i + lf] = (bf16)(orun[i] * inv);
+    if (p.lse && lf == 0 && vs == 0) p.lse[(int64_t)t * p.lse_st + h] = (Mrun + __log2f(Zrun)) * kLn2;
   }
 }
 
@@ -376,19 +389,19 @@ __global__ __launch_bounds__(kGenThreads) void prefill_generic_kernel(GenericPre
 // ---------------------------------------------------------------------------
 // Host launchers
 
-template <int DK, int DV, int NQ, int NH, int P>
+template <int DK, int DV, int NQ, int NH, int P, int VS = 1>
 static hipError_t launch_prefill_mfma(const PrefillParams& base_p, hipStream_t stream) {
   PrefillParams p = base_p;
   p.qblocks = (p.total + NQ - 1) / NQ;
   p.hsub = p.group / NH;
   p.nblocks = p.qblocks * p.hk * p.hsub;
-  constexpr int NW = NQ * NH;
+  constexpr int NW = NQ * NH * VS;
   using G = FwdGeom<DK, DV, kChunk + NQ - 1, NW>;
   constexpr bool kSlot = DK >= 256 || DV >= 256;
   size_t lds = (size_t)(P + (kSlot ? 2 : 1)) * G::SLOT;  // P + 1 ring slots (+ the short-window slot)
   const size_t red = (size_t)NW * 64 * 36 * sizeof(float);
   if (lds < red) lds = red;
-  auto kern = prefill_mfma_kernel<DK, DV, NQ, NH, P>;
+  auto kern = prefill_mfma_kernel<DK, DV, NQ, NH, P, VS>;
   hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(p.nblocks), dim3(64 * NW), lds, stream, p);
@@ -402,9 +415,10 @@ template <int DK, int DV>
 static hipError_t dispatch_prefill_mfma_d(const PrefillParams& p, hipStream_t stream) {
   const int G = p.group;
   if constexpr (DK >= 256 || DV >= 256) {
-    if (G % 4 == 0) return launch_prefill_mfma<DK, DV, 1, 4, 2>(p, stream);
-    if (G % 2 == 0) return launch_prefill_mfma<DK, DV, 2, 2, 2>(p, stream);
-    return launch_prefill_mfma<DK, DV, 4, 1, 2>(p, stream);
+    constexpr int VS = SA_PREFILL_WIDE_VS;
+    if (G % 4 == 0) return launch_prefill_mfma<DK, DV, 1, 4, 2, VS>(p, stream);
+    if (G % 2 == 0) return launch_prefill_mfma<DK, DV, 2, 2, 2, VS>(p, stream);
+    return launch_prefill_mfma<DK, DV, 4, 1, 2, VS>(p, stream);
   } else {
     constexpr int P = SA_PREFILL_DEPTH;
     if (G % 4 == 0) return launch_prefill_mfma<DK, DV, 1, 4, P>(p, stream);
