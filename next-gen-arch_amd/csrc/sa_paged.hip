@@ -57,7 +57,7 @@ struct PagedParams {
 
 constexpr int kPosCache = 1024;
 #ifndef SA_PAGED_STEP_PF
-#define SA_PAGED_STEP_PF 1
+#define SA_PAGED_STEP_PF 2
 #endif  // long-window positions of one split whose row offsets are kept in LDS
 
 template <int D, int NW, int P>
@@ -65,7 +65,7 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
   using G = FwdGeom<D, D, kChunk, NW>;
   using RB = RowBlock<D, D>;
   constexpr bool kPipelined = D <= 128 && P >= 2;  // second score tile fits the registers up to D = 128
-  constexpr int kStepPF = SA_PAGED_STEP_PF;  // V fragments read ahead of the PV MFMAs (2 and 3 measured no faster)
+  constexpr int kStepPF = SA_PAGED_STEP_PF;  // V fragments read ahead of the PV MFMAs (C5 42.0 -> 41.6 us)
   constexpr int SLOT = G::SLOT;
   constexpr int R = P + 1;
   constexpr int NI = G::NI;  // DMA instructions per wave per tile
