@@ -50,6 +50,10 @@
 extern "C" {
 #endif
 
+/* The library is built with hidden symbol visibility; the declarations below
+ * are its only exports. */
+#pragma GCC visibility push(default)
+
 typedef struct ihipStream_t* sa_stream_t; /* a hipStream_t; NULL = default stream */
 
 enum {
@@ -167,6 +171,8 @@ const char* sa_last_error(void);
 
 /* Library version string. */
 const char* sa_version(void);
+
+#pragma GCC visibility pop
 
 #ifdef __cplusplus
 }

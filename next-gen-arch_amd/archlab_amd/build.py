@@ -24,11 +24,15 @@ ARCH = os.environ.get("SA_OFFLOAD_ARCH", "gfx950")
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 generation (those forms have
 # produced silent wrong results on the target pool); the host pass warns that
 # it does not know the feature, which is harmless.
+# -fvisibility=hidden: only the C ABI (declared with default visibility in
+# the header) is exported, so two builds loaded into one process (or another
+# library) cannot interpose each other's internal functions.
 # -mno-amdgpu-ieee / -fno-honor-nans: fmax without NaN canonicalisation; the
 # kernels never produce NaN from finite inputs and use -inf explicitly.
 COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-mcode-object-version=5",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-          "-mno-amdgpu-ieee", "-fno-honor-nans", "-Wall", "-Wno-unused-function"]
+          "-mno-amdgpu-ieee", "-fno-honor-nans", "-Wall", "-Wno-unused-function",
+          "-fvisibility=hidden"]
 
 
 def hipcc() -> str:
