@@ -15,7 +15,11 @@ D=128, long window w1=512, short window w2=32), effective FLOPs
     (and on the ``--bwd-configs`` workloads, C3 and C4 by default, in
     ``"backward_configs"``);
   * ``roofline`` of the dominant kernel and ``cpu_baseline`` (the oracle
-    timed on this host's cores on a bounded sample of the same workload).
+    timed on this host's cores on a bounded sample of the same workload);
+  * beside every nominal prefill figure, ``valid_pair_flops`` and
+    ``valid_pair_tflops``: the FLOPs of the (short key, long key) pairs the
+    queries can actually see (windows cut at sequence starts), counted in
+    closed form as the reference's cost ledger does (limite_cost.py:31-45, :69-73).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
                        [--legs prefill,configs,decode,fp32,backward,cpu]
@@ -128,11 +132,13 @@ def prefill_leg(args, name=None, steps=None):
     mean_ms, med_ms, _ = _time_kernel(fn, steps or args.steps, args.warmup)
     flops = W.prefill_flops(cfg)
     tflops = flops / (mean_ms * 1e-3) / 1e12
+    valid = W.prefill_valid_flops(cfg)
     del q, k1, k2, v1, v2, cu
     torch.cuda.empty_cache()
     return {
         "name": name, "cfg": cfg, "ms": mean_ms, "median_ms": med_ms, "tflops": tflops, "flops": flops,
-        "bytes": W.prefill_bytes(cfg),
+        "bytes": W.prefill_bytes(cfg), "valid_pair_flops": valid,
+        "valid_pair_tflops": valid / (mean_ms * 1e-3) / 1e12,
     }
 
 
@@ -157,8 +163,9 @@ def configs_leg(args):
     for name in [c for c in args.configs.split(",") if c]:
         pre = prefill_leg(args, name)
         res = {"workload": _workload_label(pre["cfg"]), "ms_per_step": round(pre["ms"], 4),
-               "tflops": round(pre["tflops"], 2), "flops_per_step": pre["flops"], "kernel": "prefill_mfma_kernel",
-               "roofline": _prefill_roofline(pre)}
+               "tflops": round(pre["tflops"], 2), "flops_per_step": pre["flops"],
+               "valid_pair_flops": pre["valid_pair_flops"], "valid_pair_tflops": round(pre["valid_pair_tflops"], 2),
+               "kernel": "prefill_mfma_kernel", "roofline": _prefill_roofline(pre)}
         if "cpu" in set(args.legs.split(",")):
             res["cpu_baseline"] = cpu_leg(args, pre["cfg"])
         out[name] = res
@@ -292,12 +299,14 @@ def backward_leg(args, fwd_ms, workload=None):
             fwd_ms, _, _ = _time_kernel(fwd, args.bwd_steps, 3)
     bwd_ms = mean_ms - fwd_ms
     flops = 2.0 * W.prefill_flops(cfg)
+    valid = 2.0 * W.prefill_valid_flops(cfg)
     del xs, dy, q, k1, k2, v1, v2
     torch.cuda.empty_cache()
     return {
         "workload": cfg.name, "fwd_bwd_ms": mean_ms, "fwd_ms": fwd_ms, "bwd_ms": bwd_ms,
         "bwd_flops": flops, "bwd_tflops": flops / (bwd_ms * 1e-3) / 1e12,
         "bwd_frac_of_peak": flops / (bwd_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+        "bwd_valid_pair_flops": valid, "bwd_valid_pair_tflops": valid / (bwd_ms * 1e-3) / 1e12,
         "kernels": "bwd_dq_mfma_kernel, bwd_dkv1_mfma_kernel, bwd_dkv2_mfma_kernel (+ bwd_delta_kernel)",
     }
 
@@ -426,6 +435,8 @@ def main():
         out["value"] = round(pre["tflops"], 2)
         out["ms_per_step"] = round(pre["ms"], 4)
         out["config"] = {"workload": _workload_label(cfg), "flops_per_step": pre["flops"],
+                         "valid_pair_flops": pre["valid_pair_flops"],
+                         "valid_pair_tflops": round(pre["valid_pair_tflops"], 2),
                          "kernel": "prefill_mfma_kernel"}
         out["roofline"] = _prefill_roofline(pre)
         _progress(f"prefill {pre['name']}: {pre['ms']:.3f} ms, {pre['tflops']:.1f} TFLOP/s")

@@ -29,7 +29,8 @@
  *                             head) delta and dlse rows and, for bf16 calls
  *                             whose short window is one 32-row group, the
  *                             dk1 partials written by the dq pass (at most
- *                             8 GiB; beyond that a separate dk1 pass runs).
+ *                             8 GiB; beyond that, or with
+ *                             SA_FLAG_SEPARATE_DK1, a separate dk1 pass runs).
  *
  * Conventions
  *   - All pointers are device pointers; strides are in ELEMENTS; the last
@@ -54,6 +55,14 @@
 extern "C" {
 #endif
 
+/* Version of the argument structs and enums below.  It changes whenever a
+ * struct gains, loses or moves a field or an enum value changes meaning, so a
+ * caller built against another header can detect the mismatch at load time
+ * (compare sa_abi_version() with this value before the first call; the
+ * structs carry no size field, and a shorter caller struct would otherwise
+ * be read past its end).  3: fp16 paged caches, SA_FLAG_SEPARATE_DK1. */
+#define SIMPLICIAL_MI355X_ABI_VERSION 3
+
 /* The library is built with hidden symbol visibility; the declarations below
  * are its only exports. */
 #pragma GCC visibility push(default)
@@ -67,11 +76,20 @@ enum {
   SA_ERR_HIP = 3          /* HIP runtime error at launch (RuntimeError) */
 };
 
-enum { SA_DTYPE_F32 = 0, SA_DTYPE_BF16 = 1 };
+/* Element types.  SA_DTYPE_F16 is accepted for the paged caches only (the
+ * reference's paged Triton loads read any float cache, simplicial_paged.py:42-52);
+ * queries and the prefill tensors are float32 or bfloat16 as in the reference
+ * (simplicial_attention.py:87-88, simplicial_paged.py:88). */
+enum { SA_DTYPE_F32 = 0, SA_DTYPE_BF16 = 1, SA_DTYPE_F16 = 2 };
 enum { SA_INDEX_I32 = 0, SA_INDEX_I64 = 1 };
 
 enum {
-  SA_FLAG_FORCE_GENERIC = 1 /* use the portable (non-MFMA) kernel; for cross-checks */
+  SA_FLAG_FORCE_GENERIC = 1, /* use the portable (non-MFMA) kernel; for cross-checks */
+  /* sa_prefill_bwd only: compute dk1 in a pass of its own instead of from
+   * partials written by the dq pass.  The workspace then holds no dk1
+   * partials (those take 16-17.5x the bytes of q); the backward runs one
+   * more recomputation pass (about 20 % more time at the benchmark shape). */
+  SA_FLAG_SEPARATE_DK1 = 2
 };
 
 typedef struct sa_prefill_args {
@@ -107,7 +125,7 @@ typedef struct sa_prefill_args {
 typedef struct sa_paged_args {
   const void* q; /* [tokens, heads_q, D], q_dtype */
   int64_t q_stride_t, q_stride_h;
-  const void* short_cache; /* [2 (K,V), blocks, block_size, heads_kv, D], cache_dtype */
+  const void* short_cache; /* [2 (K,V), blocks, block_size, heads_kv, D], cache_dtype (f32, bf16 or f16) */
   int64_t sc_stride[4];    /* element strides of dims 0..3 */
   const void* long_cache; /* same geometry, long_cache_dtype */
   int64_t lc_stride[4];
@@ -128,11 +146,11 @@ typedef struct sa_paged_args {
   int32_t splits;        /* long-window splits; <= 0 selects automatically */
   float scale;
   int32_t q_dtype;           /* SA_DTYPE_* of q */
-  int32_t cache_dtype;       /* SA_DTYPE_* of short_cache */
+  int32_t cache_dtype;       /* SA_DTYPE_* of short_cache (F32, BF16 or F16) */
   int32_t table_index_dtype; /* SA_INDEX_* of short_table */
   int32_t token_index_dtype; /* SA_INDEX_* of token_seq */
   int32_t flags;
-  int32_t long_cache_dtype;       /* SA_DTYPE_* of long_cache */
+  int32_t long_cache_dtype;       /* SA_DTYPE_* of long_cache (F32, BF16 or F16) */
   int32_t long_table_index_dtype; /* SA_INDEX_* of long_table */
   int32_t token_pos_index_dtype;  /* SA_INDEX_* of token_pos */
   /* Optional per-token window limits, int32 [tokens][2] on the device, or
@@ -171,9 +189,10 @@ typedef struct sa_prefill_bwd_args {
  * [tokens, heads_q] rows, plus the dq pass's dk1 partials where it produces
  * dk1 (bf16, head_dim and value_dim each 64 or 128, or head_dim 256 over
  * value_dim 128 / 256; short window <= 32; 16-17.5x the bytes of q, up to
- * 8 GiB), plus, for short windows of 65-128 (33-64 at head_dim 256), the
- * fp32 dk2 and dv2 sums of the first of two dk2 / dv2 launches
- * ([tokens][heads_kv][head_dim + value_dim]). */
+ * 8 GiB; none with SA_FLAG_SEPARATE_DK1 in args->fwd.flags), plus, for
+ * short windows of 65-128 (33-64 at head_dim 256), the fp32 dk2 and dv2 sums
+ * of the first of two dk2 / dv2 launches ([tokens][heads_kv][head_dim +
+ * value_dim]). */
 size_t sa_prefill_bwd_workspace_bytes(const sa_prefill_bwd_args* args);
 
 /* Backward of sa_prefill_fwd: writes dq, dk1, dk2, dv1, dv2 (each exactly
@@ -214,6 +233,9 @@ const char* sa_last_error(void);
 
 /* Library version string. */
 const char* sa_version(void);
+
+/* SIMPLICIAL_MI355X_ABI_VERSION of the header the library was built from. */
+int sa_abi_version(void);
 
 #pragma GCC visibility pop
 

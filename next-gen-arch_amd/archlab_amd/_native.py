@@ -17,9 +17,12 @@ LIB_NAME = "libsimplicial_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 SA_OK, SA_ERR_INVALID, SA_ERR_UNSUPPORTED, SA_ERR_HIP = 0, 1, 2, 3
-SA_DTYPE_F32, SA_DTYPE_BF16 = 0, 1
+SA_DTYPE_F32, SA_DTYPE_BF16, SA_DTYPE_F16 = 0, 1, 2
 SA_INDEX_I32, SA_INDEX_I64 = 0, 1
 SA_FLAG_FORCE_GENERIC = 1
+SA_FLAG_SEPARATE_DK1 = 2
+# SIMPLICIAL_MI355X_ABI_VERSION of the header these struct layouts mirror
+ABI_VERSION = 3
 
 _i64, _i32, _f32, _vp = ctypes.c_int64, ctypes.c_int32, ctypes.c_float, ctypes.c_void_p
 
@@ -78,7 +81,7 @@ class PrefillBwdArgs(ctypes.Structure):
 EXPORTS = ("sa_prefill_fwd", "sa_paged_fwd", "sa_paged_workspace_bytes", "sa_paged_splits",
            "sa_prefill_kernel", "sa_paged_kernel", "sa_last_error", "sa_version",
            "sa_prefill_bwd", "sa_prefill_bwd_workspace_bytes", "sa_paged_fwd_noalloc",
-           "sa_prefill_workspace_bytes")
+           "sa_prefill_workspace_bytes", "sa_abi_version")
 
 _lib = None
 _lock = threading.Lock()
@@ -125,6 +128,12 @@ def load():
         lib.sa_last_error.restype = ctypes.c_char_p
         lib.sa_version.argtypes = []
         lib.sa_version.restype = ctypes.c_char_p
+        lib.sa_abi_version.argtypes = []
+        lib.sa_abi_version.restype = ctypes.c_int
+        if lib.sa_abi_version() != ABI_VERSION:
+            raise RuntimeError(
+                f"{LIB_NAME} implements ABI {lib.sa_abi_version()}, this binding expects {ABI_VERSION}; "
+                "rebuild the library (`python -m archlab_amd.build`)")
         _lib = lib
     return _lib
 
@@ -155,6 +164,16 @@ def dtype_code(dtype) -> int:
     if dtype == torch.bfloat16:
         return SA_DTYPE_BF16
     raise ValueError("kernel supports float32/bfloat16")
+
+
+def cache_dtype_code(dtype) -> int:
+    """Element type of a paged cache: float32, bfloat16 or float16 (the
+    reference's paged loads read any float cache, simplicial_paged.py:42-52)."""
+    if dtype == torch.float16:
+        return SA_DTYPE_F16
+    if dtype in (torch.float32, torch.bfloat16):
+        return dtype_code(dtype)
+    raise ValueError("kernel supports float32/bfloat16/float16 caches")
 
 
 def index_code(dtype) -> int:

@@ -150,7 +150,14 @@ def _backward(q, k1, k2, v1, v2, out, lse, dout, dlse, short_window, long_window
         dv1=dv1.data_ptr(), dv2=dv2.data_ptr(), dv_stride_t=dv1.stride(0), dv_stride_h=dv1.stride(1),
         dlse=dlse.data_ptr() if dlse is not None else None, dlse_stride_t=hq)
     nbytes = lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args))
-    workspace = torch.empty(max(nbytes, 1) + 256, device=q.device, dtype=torch.uint8)
+    try:
+        workspace = torch.empty(max(nbytes, 1) + 256, device=q.device, dtype=torch.uint8)
+    except torch.cuda.OutOfMemoryError:
+        # the dq pass's dk1 partials (16-17.5x the bytes of q) do not fit:
+        # compute dk1 in its own pass, with the small workspace
+        args.fwd.flags |= _native.SA_FLAG_SEPARATE_DK1
+        nbytes = lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args))
+        workspace = torch.empty(max(nbytes, 1) + 256, device=q.device, dtype=torch.uint8)
     aligned = (workspace.data_ptr() + 255) & ~255
     with torch.cuda.device(q.device):
         _native.check(lib.sa_prefill_bwd(ctypes.byref(args), aligned, nbytes, _native.stream_handle(q.device)))

@@ -8,8 +8,10 @@
 * ``packed_simplicial_decode`` (simplicial_packed.py:290-338): one fp32 query
   against explicit windows of at most 16 short rows.
 
-Both keep the reference's argument checks and messages.  They run on the
-portable fp32 kernels of the library (no MFMA path exists for fp32).
+Both keep the reference's argument checks and messages.  The prefill runs on
+the matrix cores with every fp32 operand split into hi + lo bf16 terms
+(fp32-accurate, within 1e-4 of the fp64 oracle); its backward and the
+decode's fp32 windows run on the library's kernels for fp32 inputs.
 """
 
 from __future__ import annotations

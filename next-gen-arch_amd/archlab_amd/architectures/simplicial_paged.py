@@ -41,8 +41,8 @@ def _paged_args(q, short_cache, long_cache, block_table, long_block_table, token
         short_blocks=short_cache.shape[1], long_blocks=long_cache.shape[1],
         short_window=_native.window(short_window), long_window=_native.window(long_window),
         splits=0 if splits is None else min(int(splits), _native.INT32_MAX), scale=float(scale),
-        q_dtype=_native.dtype_code(q.dtype), cache_dtype=_native.dtype_code(short_cache.dtype),
-        long_cache_dtype=_native.dtype_code(long_cache.dtype),
+        q_dtype=_native.dtype_code(q.dtype), cache_dtype=_native.cache_dtype_code(short_cache.dtype),
+        long_cache_dtype=_native.cache_dtype_code(long_cache.dtype),
         table_index_dtype=_native.index_code(block_table.dtype),
         long_table_index_dtype=_native.index_code(long_block_table.dtype),
         token_index_dtype=_native.index_code(token_seq.dtype),
@@ -83,10 +83,11 @@ def simplicial_paged_attention(q, short_cache, long_cache, block_table, token_se
             or token_seq.shape != (tokens,) or token_pos.shape != (tokens,)
             or block_table.ndim != 2 or long_block_table.ndim != 2):
         raise ValueError("invalid paged simplicial inputs")
-    # the reference reads the caches in any dtype its loads accept; this
-    # library's kernels take float32 and bfloat16 caches (each on its own)
-    if any(x.dtype not in (torch.float32, torch.bfloat16) for x in (short_cache, long_cache)):
-        raise ValueError("kernel supports float32/bfloat16 caches")
+    # the reference reads the caches in any float dtype its loads accept
+    # (simplicial_paged.py:42-52); this library takes float32, bfloat16 and
+    # float16 caches, each axis on its own
+    if any(x.dtype not in (torch.float32, torch.bfloat16, torch.float16) for x in (short_cache, long_cache)):
+        raise ValueError("kernel supports float32/bfloat16/float16 caches")
     if (q.stride(-1) != 1 or short_cache.stride(-1) != 1 or long_cache.stride(-1) != 1
             or block_table.stride(-1) != 1 or long_block_table.stride(-1) != 1):
         raise ValueError("innermost dimensions must be contiguous")

@@ -17,6 +17,8 @@ from dataclasses import dataclass, field
 
 import torch
 
+from . import cost
+
 
 @dataclass(frozen=True)
 class PrefillConfig:
@@ -159,6 +161,24 @@ def _randn_chunked(shape, generator, device, dtype):
 def prefill_flops(cfg: PrefillConfig) -> float:
     """Nominal FLOPs 4 * B * H * S * w1 * w2 * D (full windows)."""
     return 4.0 * cfg.batch * cfg.heads_q * cfg.seqlen * cfg.w1 * cfg.w2 * cfg.dim
+
+
+def sequence_lengths(cfg: PrefillConfig) -> list[int]:
+    """Lengths of the independent sequences of a prefill configuration."""
+    if cfg.varlen_seqs:
+        return list(cfg.lengths or varlen_lengths(cfg.tokens, cfg.varlen_seqs, cfg.varlen_seed))
+    return [cfg.seqlen] * cfg.batch
+
+
+def prefill_triples(cfg: PrefillConfig) -> int:
+    """Scored (short key, long key) pairs summed over every query of the
+    configuration (windows cut at each sequence start; limite_cost.py:38-45)."""
+    return cost.sequence_triples(sequence_lengths(cfg), cfg.w2, cfg.w1)
+
+
+def prefill_valid_flops(cfg: PrefillConfig) -> float:
+    """Forward FLOPs of the valid pairs only: 4 * HQ * D per scored pair."""
+    return cost.forward_flops(cfg.heads_q, cfg.dim, prefill_triples(cfg))
 
 
 def prefill_bytes(cfg: PrefillConfig) -> float:

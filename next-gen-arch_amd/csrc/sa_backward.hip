@@ -535,11 +535,12 @@ static bool dk1_fused_shape(const sa_prefill_bwd_args* a) {
   const sa_prefill_args& f = a->fwd;
   const bool narrow = (f.head_dim == 64 || f.head_dim == 128) && (f.value_dim == 64 || f.value_dim == 128);
   const bool wide = f.head_dim == 256 && (f.value_dim == 128 || f.value_dim == 256);
-  return f.dtype == SA_DTYPE_BF16 && !(f.flags & SA_FLAG_FORCE_GENERIC) && (narrow || wide) &&
-         f.short_window <= 32 && f.heads_kv > 0;
+  return f.dtype == SA_DTYPE_BF16 && !(f.flags & (SA_FLAG_FORCE_GENERIC | SA_FLAG_SEPARATE_DK1)) &&
+         (narrow || wide) && f.short_window <= 32 && f.heads_kv > 0;
 }
-// The partials take 16-17.5x the bytes of q; past kDk1PartialCap the separate
-// dk1 pass runs instead (no workspace beyond the delta / dlse rows).
+// The partials take 16-17.5x the bytes of q; past kDk1PartialCap (or with
+// SA_FLAG_SEPARATE_DK1, for callers short of memory) the separate dk1 pass
+// runs instead (no workspace beyond the delta / dlse rows).
 constexpr size_t kDk1PartialCap = (size_t)8 << 30;
 static size_t dk1_partial_bytes(const sa_prefill_bwd_args* a) {
   if (!dk1_fused_shape(a)) return 0;

@@ -39,15 +39,9 @@ namespace sa {
 namespace {
 
 // LDS fragments read ahead of their MFMA in each pass (see BwdOps)
-#ifndef SA_DQ_PF
-#define SA_DQ_PF 1
-#endif
-#ifndef SA_DK1_PF
-#define SA_DK1_PF 1
-#endif
-#ifndef SA_DKV2_PF
-#define SA_DKV2_PF 2
-#endif
+constexpr int kDqPF = 1;    // dq pass
+constexpr int kDk1PF = 1;   // dk1 / dv1 pass (dv1 reads two ahead)
+constexpr int kDkv2PF = 2;  // dk2 / dv2 pass
 
 // Wave-level tile products used by the backward passes (D = head dim).
 template <int D>
@@ -314,8 +308,8 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dq_mfma_ke
       const int klo = active ? max(lo2 - kfirst, 0) : kChunk;
       const int khi = active ? min(t - kfirst, kChunk - 1) : -1;
       const char* slot = lds + (c % R) * G::SLOT;
-      const floatx16 s = OPK::template rows_x<G::RSK, SA_DQ_PF>(slot, qo, lane, ra.a);
-      const floatx16 dp = OPV::template rows_x<G::RSV, SA_DQ_PF>(slot + G::VOFF, qo, lane, rbv.a);
+      const floatx16 s = OPK::template rows_x<G::RSK, kDqPF>(slot, qo, lane, ra.a);
+      const floatx16 dp = OPV::template rows_x<G::RSV, kDqPF>(slot + G::VOFF, qo, lane, rbv.a);
       // register r holds chunk key 8*(r/4) + r%4 + 4*half of column j = this lane's row
       const int lo_h = klo - 4 * half, hi_h = khi - 4 * half;
       float ds[16];
@@ -334,7 +328,7 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dq_mfma_ke
       }
       bf16x8 pb0, pb1;
       OPK::pack_c(ds, pb0, pb1);
-      OPK::template tr_acc<G::RSK, SA_DQ_PF>(dA, slot, qo, lane, pb0, pb1);  // dA^T += K2^T · dS^T
+      OPK::template tr_acc<G::RSK, kDqPF>(dA, slot, qo, lane, pb0, pb1);  // dA^T += K2^T · dS^T
     }
     wait_vmcnt<0>();
     block_barrier();  // ring reads done (LDS reused below)
@@ -630,7 +624,7 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dkv1_mfma_
         const int khi = min(n + p.wl - 1 - kChunk * c, kChunk - 1);
         const char* slot = lds + (c % R) * G::SLOT;
         // dv1 launch (registers to spare): reads two MFMAs ahead
-        constexpr int kPF = kDV ? 2 : SA_DK1_PF;
+        constexpr int kPF = kDV ? 2 : kDk1PF;
         const floatx16 sv = OPK::template rows_x<G::RSK, kPF>(slot, qo, lane, ra.a);
         floatx16 dp;
         if constexpr (kDK) dp = OPV::template rows_x<G::RSV>(slot + G::VOFF, qo, lane, rbv.a);
@@ -813,7 +807,7 @@ __global__ __launch_bounds__(64 * NWK, DK > 128 ? 1 : 2) void bwd_dkv2_mfma_kern
   constexpr int RPW = 32 / NWK;   // A / B rows formed per wave and step
   // LDS reads in flight ahead of their MFMA: with two waves per SIMD, one
   // read ahead leaves each step's three MFMA chains waiting on LDS latency
-  constexpr int kPF = SA_DKV2_PF;
+  constexpr int kPF = kDkv2PF;
   static_assert(kDK || kDV, "one output per launch");
   constexpr int XW = kDK ? DK : DV;        // width of the gradient accumulated
   using OPK = BwdOps<DK>;

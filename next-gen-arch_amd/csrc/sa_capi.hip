@@ -150,9 +150,12 @@ static int check_paged(const sa_paged_args* a) {
       !pow2_dim(a->head_dim, 16, 256))
     return fail(SA_ERR_INVALID, "incompatible paged simplicial geometry");
   if (a->heads_q / a->heads_kv > 128) return fail(SA_ERR_INVALID, "at most 128 query heads per KV group");
+  // queries fp32 / bf16 (simplicial_paged.py:88); caches also fp16 (the
+  // reference's loads take any float cache and cast, :42-52)
   auto fp = [](int32_t d) { return d == SA_DTYPE_F32 || d == SA_DTYPE_BF16; };
+  auto cf = [](int32_t d) { return d == SA_DTYPE_F32 || d == SA_DTYPE_BF16 || d == SA_DTYPE_F16; };
   auto ix = [](int32_t d) { return d == SA_INDEX_I32 || d == SA_INDEX_I64; };
-  if (!fp(a->q_dtype) || !fp(a->cache_dtype) || !fp(a->long_cache_dtype) || !ix(a->table_index_dtype) ||
+  if (!fp(a->q_dtype) || !cf(a->cache_dtype) || !cf(a->long_cache_dtype) || !ix(a->table_index_dtype) ||
       !ix(a->long_table_index_dtype) || !ix(a->token_index_dtype) || !ix(a->token_pos_index_dtype))
     return fail(SA_ERR_INVALID, "invalid paged simplicial inputs");
   if (a->tokens > 0 && (a->num_seqs < 1 || a->short_table_width < 1 || a->long_table_width < 1 ||
@@ -201,7 +204,9 @@ extern "C" {
 
 const char* sa_last_error(void) { return sa::g_last_error.c_str(); }
 
-const char* sa_version(void) { return "simplicial_mi355x 0.1 (gfx950)"; }
+const char* sa_version(void) { return "simplicial_mi355x 0.3 (gfx950)"; }
+
+int sa_abi_version(void) { return SIMPLICIAL_MI355X_ABI_VERSION; }
 
 int sa_prefill_fwd(const sa_prefill_args* a, sa_stream_t stream) {
   int rc = sa::check_prefill(a);

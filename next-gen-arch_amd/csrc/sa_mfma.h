@@ -186,15 +186,6 @@ __device__ __forceinline__ void lds_wait_n(shortx4& a, shortx4& b) {
   asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
 }
 
-#ifndef SA_MFMA_PRIO
-#define SA_MFMA_PRIO 0
-#endif
-// Wave priority around the MFMA groups of a chunk (0: unchanged).
-template <int LEVEL>
-__device__ __forceinline__ void mfma_prio() {
-  if constexpr (SA_MFMA_PRIO != 0) __builtin_amdgcn_s_setprio(LEVEL);
-}
-
 // Row sum of one chunk's probabilities beyond which the chunk loop moves the
 // reference max (see RowBlock::chunk): probabilities stay below 2^24, far
 // inside the fp32 range of the accumulators, and bf16 rounding is relative.
@@ -245,9 +236,16 @@ __device__ __forceinline__ void pack_bf16_split(float p0, float p1, uint32_t& hi
 //
 // The softmax keeps ONE running reference max for the wave's 32 rows (the
 // joint softmax of the reference has one max per query and head, and every
-// row of the wave belongs to the same query and head), moved lazily: only
-// when some row's chunk max exceeds it by more than 2^8.  Rows outside the
-// query's short window get p = 0 through an infinite exponent bias.
+// row of the wave belongs to the same query and head), moved lazily, by a
+// two-level rule.  The chunk loop (chunk) computes probabilities against the
+// current reference without a chunk maximum; only when some row's chunk sum
+// passes kLazyBound = 2^24 (a first valid chunk, a score far above the
+// reference, an overflow) does it take the chunk maxima and call rescale,
+// which moves the reference only when a row's maximum exceeds it by more than
+// 8 in the log2 domain (a factor 2^8), and then to the largest such maximum,
+// and recomputes the chunk.  The pipelined step (step) calls rescale with
+// every chunk's maximum.  Rows outside the query's short window get p = 0
+// through an infinite exponent bias.
 //
 // OT selects the output layout.  !OT: O^T = V^T · P^T, lane = A row n,
 // registers = d (32*db + acc_row(r, half)).  OT: O = P · V (the same two
@@ -461,7 +459,6 @@ struct RowBlock {
         bf16x8 kq[DK / 16];
         kq[0] = *(const bf16x8*)kp;
         if (DK / 16 > 1) kq[1] = *(const bf16x8*)(kp + 32);
-        mfma_prio<1>();
 #pragma unroll
         for (int t = 0; t < DK / 16; ++t) {
           if (t + 2 < DK / 16) kq[t + 2] = *(const bf16x8*)(kp + 32 * (t + 2));
@@ -469,7 +466,6 @@ struct RowBlock {
           s = qk_mfma(kq[t], t, s);
           __builtin_amdgcn_sched_barrier(0);
         }
-        if constexpr (SA_MFMA_PRIO != 2) mfma_prio<0>();
       }
     }
     const bool masked = key_lo > 0 || key_hi < kChunk - 1;
@@ -565,7 +561,6 @@ struct RowBlock {
     shortx4 v1, v2;
     vread<RSV, 0>(vp, v1, v2);
     lds_wait(v1, v2);
-    if constexpr (SA_MFMA_PRIO == 1) mfma_prio<1>();
     static_for<0, kSteps>([&](auto st) {
       constexpr int step = decltype(st)::value;
       shortx8 vv = {v1[0], v1[1], v1[2], v1[3], v2[0], v2[1], v2[2], v2[3]};
@@ -582,7 +577,6 @@ struct RowBlock {
         v2 = n2;
       }
     });
-    mfma_prio<0>();
   }
 
   // ---- Software-pipelined form -------------------------------------------
@@ -624,9 +618,9 @@ struct RowBlock {
   }
 
   // Lazy rescale: move the wave's reference max only when some row's scaled
-  // chunk max `cmax` (rows outside the window excluded) exceeds it by more
-  // than 2^8; then to the largest such max, and every row is rescaled by the
-  // same factor.
+  // chunk max `cmax` (rows outside the window excluded, log2 domain) exceeds
+  // it by more than 8 (a factor 2^8); then to the largest such max, and every
+  // row is rescaled by the same factor.
   __device__ __forceinline__ void rescale(float cmax) {
     const float cand = valid ? cmax : -INFINITY;
     const bool grow = cand > m + 8.0f;

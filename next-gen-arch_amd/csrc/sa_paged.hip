@@ -58,9 +58,6 @@ struct PagedParams {
 
 constexpr int kPosCache = 1024;            // long-window positions whose row offsets are kept in LDS
 constexpr int kSegChunks = kPosCache / kChunk;  // chunks of one such segment
-#ifndef SA_PAGED_STEP_PF
-#define SA_PAGED_STEP_PF 2
-#endif
 
 // MULTI: the split may span more than one segment of kSegChunks chunks (long
 // windows); without it the segment loop below runs exactly once and folds
@@ -73,7 +70,7 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
   using G = FwdGeom<D, D, kChunk, NW>;
   using RB = RowBlock<D, D, QF32>;
   constexpr bool kPipelined = D <= 128 && P >= 2;  // second score tile fits the registers up to D = 128
-  constexpr int kStepPF = SA_PAGED_STEP_PF;  // V fragments read ahead of the PV MFMAs (C5 42.0 -> 41.6 us)
+  constexpr int kStepPF = 2;  // V fragments read ahead of the PV MFMAs (C5 42.0 -> 41.6 us)
   constexpr int SLOT = G::SLOT;
   constexpr int R = P + 1;
   constexpr int NI = G::NI;  // DMA instructions per wave per tile
@@ -518,10 +515,7 @@ size_t paged_workspace_bytes(const sa_paged_args* a, int splits) {
   return b + 2 * m;
 }
 
-#ifndef SA_PAGED_DEPTH
-#define SA_PAGED_DEPTH 2
-#endif
-constexpr int kPagedDepth = SA_PAGED_DEPTH;  // tiles in flight per workgroup (2 workgroups fit one CU)
+constexpr int kPagedDepth = 2;  // tiles in flight per workgroup (2 workgroups fit one CU)
 
 template <int D, int NW, bool QF32>
 static hipError_t launch_paged_mfma_t(PagedParams p, hipStream_t stream) {
@@ -547,6 +541,38 @@ static hipError_t launch_paged_mfma_d(const PagedParams& p, int nw, hipStream_t 
   if (nw == 4) return launch_paged_mfma_t<D, 4, QF32>(p, stream);
   if (nw == 2) return launch_paged_mfma_t<D, 2, QF32>(p, stream);
   return launch_paged_mfma_t<D, 1, QF32>(p, stream);
+}
+
+// Portable kernel for one combination of query and cache element types
+// (caches: fp32, bf16 or fp16, each axis on its own).
+template <typename QT, typename SCT, typename LCT>
+static hipError_t launch_paged_generic_t(const GenericPagedParams& gp, const sa_paged_args* a, size_t lds,
+                                         hipStream_t stream) {
+  auto kern = paged_generic_kernel<QT, SCT, LCT>;
+  hipError_t e = set_lds_limit((const void*)kern, lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(a->tokens, a->heads_q), dim3(kGenThreads), lds, stream, gp);
+  return hipGetLastError();
+}
+
+template <typename QT, typename SCT>
+static hipError_t launch_paged_generic_l(const GenericPagedParams& gp, const sa_paged_args* a, size_t lds,
+                                         hipStream_t stream) {
+  switch (a->long_cache_dtype) {
+    case SA_DTYPE_F32: return launch_paged_generic_t<QT, SCT, float>(gp, a, lds, stream);
+    case SA_DTYPE_F16: return launch_paged_generic_t<QT, SCT, _Float16>(gp, a, lds, stream);
+    default: return launch_paged_generic_t<QT, SCT, bf16>(gp, a, lds, stream);
+  }
+}
+
+template <typename QT>
+static hipError_t launch_paged_generic_q(const GenericPagedParams& gp, const sa_paged_args* a, size_t lds,
+                                         hipStream_t stream) {
+  switch (a->cache_dtype) {
+    case SA_DTYPE_F32: return launch_paged_generic_l<QT, float>(gp, a, lds, stream);
+    case SA_DTYPE_F16: return launch_paged_generic_l<QT, _Float16>(gp, a, lds, stream);
+    default: return launch_paged_generic_l<QT, bf16>(gp, a, lds, stream);
+  }
 }
 
 hipError_t launch_paged(const sa_paged_args* a, int splits, void* ws, size_t ws_bytes, hipStream_t stream) {
@@ -675,27 +701,8 @@ hipError_t launch_paged(const sa_paged_args* a, int splits, void* ws, size_t ws_
   gp.lse = a->lse;
   gp.hq = a->heads_q;
   const size_t lds = gen_lds_bytes(gp.d, gp.d);
-  dim3 grid(a->tokens, a->heads_q);
-  hipError_t e;
-#define SA_LAUNCH_GP(QT, SCT, LCT)                                                                           \
-  do {                                                                                                       \
-    auto kern = paged_generic_kernel<QT, SCT, LCT>;                                                          \
-    e = set_lds_limit((const void*)kern, lds);                                                               \
-    if (e != hipSuccess) return e;                                                                           \
-    hipLaunchKernelGGL(kern, grid, dim3(kGenThreads), lds, stream, gp);                                      \
-  } while (0)
-  const bool qf = a->q_dtype == SA_DTYPE_F32, sf = a->cache_dtype == SA_DTYPE_F32,
-             lf = a->long_cache_dtype == SA_DTYPE_F32;
-  if (qf && sf && lf) SA_LAUNCH_GP(float, float, float);
-  else if (qf && sf) SA_LAUNCH_GP(float, float, bf16);
-  else if (qf && lf) SA_LAUNCH_GP(float, bf16, float);
-  else if (qf) SA_LAUNCH_GP(float, bf16, bf16);
-  else if (sf && lf) SA_LAUNCH_GP(bf16, float, float);
-  else if (sf) SA_LAUNCH_GP(bf16, float, bf16);
-  else if (lf) SA_LAUNCH_GP(bf16, bf16, float);
-  else SA_LAUNCH_GP(bf16, bf16, bf16);
-#undef SA_LAUNCH_GP
-  return hipGetLastError();
+  return a->q_dtype == SA_DTYPE_F32 ? launch_paged_generic_q<float>(gp, a, lds, stream)
+                                    : launch_paged_generic_q<bf16>(gp, a, lds, stream);
 }
 
 }  // namespace sa

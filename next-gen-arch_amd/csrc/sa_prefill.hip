@@ -64,15 +64,11 @@ struct PrefillParams {
   FastDiv qbd, hsd, sld;  // division by qblocks, hsub and seqlen
 };
 
-#ifndef SA_PREFILL_WAVES_PER_SIMD
-#define SA_PREFILL_WAVES_PER_SIMD 3
-#endif
+constexpr int kPrefillWavesPerSimd = 3;  // widths <= 128, bf16
 // V fragments read ahead of the PV MFMAs in the chunk loop (2 measured
 // 0.1-0.9 % ahead of 3 and 4); reading K fragments further ahead than one
 // spills in the loop
-#ifndef SA_PREFILL_CHUNK_PF
-#define SA_PREFILL_CHUNK_PF 2
-#endif
+constexpr int kPrefillChunkPF = 2;
 
 // One wave per (token, head), NQ x NH = 4 of them per workgroup; one K/V
 // tile in flight (a two-slot ring).
@@ -81,7 +77,7 @@ struct PrefillParams {
 // k2, v2 and v1 arrive as rows of hi and lo terms, P is split the same way,
 // and every product runs on three term pairs; the output is fp32.
 template <int DK, int DV, int NQ, int NH, bool F32 = false>
-__global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 2 : (F32 ? 2 : SA_PREFILL_WAVES_PER_SIMD)))
+__global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 2 : (F32 ? 2 : kPrefillWavesPerSimd)))
 void prefill_mfma_kernel(PrefillParams p) {
   static_assert(NQ * NH == 4, "4 (token, head) pairs per block");
   constexpr int NW = NQ * NH;
@@ -313,7 +309,7 @@ void prefill_mfma_kernel(PrefillParams p) {
         const bool active = qvalid && c >= cfirst;
         const int kfirst = t - p.wl + 1 + kChunk * c;  // key of this wave's chunk row 0
         const char* slot = slot_of(c);
-        rb.template chunk<G::RSK, G::RSV, SA_PREFILL_CHUNK_PF>(slot, slot + G::VOFF, qo, lane, p.sl2,
+        rb.template chunk<G::RSK, G::RSV, kPrefillChunkPF>(slot, slot + G::VOFF, qo, lane, p.sl2,
                                                                active ? max(lo2 - kfirst, 0) : kChunk,
                                                                active ? min(t - kfirst, kChunk - 1) : -1);
       }

@@ -228,6 +228,28 @@ def test_backward_bf16_dk1_from_dq_matches_portable(cuda):
         assert err <= bound, name
 
 
+def test_backward_bf16_separate_dk1_when_partials_do_not_fit(cuda, monkeypatch):
+    """When the workspace with the dq pass's dk1 partials cannot be allocated,
+    the shim asks again with SA_FLAG_SEPARATE_DK1 (no partials) and dk1 comes
+    from its own pass: gradients still match the fp64 oracle."""
+    import archlab_amd.architectures.simplicial_attention as shim
+    real_empty = torch.empty
+    refused = []
+
+    def empty(*size, **kw):
+        n = size[0] if size and isinstance(size[0], int) else None
+        if kw.get("dtype") is torch.uint8 and n is not None and n > (1 << 20):
+            refused.append(n)
+            raise torch.cuda.OutOfMemoryError("workspace refused by the test")
+        return real_empty(*size, **kw)
+
+    monkeypatch.setattr(shim.torch, "empty", empty)
+    _run(cuda, 1, 200, 4, 4, 128, 32, 96, torch.bfloat16, seed=77)
+    _run(cuda, 2, 61, 6, 2, 64, 20, 70, torch.bfloat16, seed=78)
+    monkeypatch.undo()
+    assert len(refused) == 2, refused  # one refused partials workspace per call, then the small one
+
+
 # ---- dk2 / dv2 on the matrix cores with short windows of 33-64 (two 32-row
 # groups of short keys per step) ----------------------------------------------------
 

@@ -33,6 +33,9 @@ def test_library_exports_every_declared_symbol():
     # hidden visibility: the header's functions are the only exported code
     assert exported == set(declared), sorted(exported ^ set(declared))
     assert lib.sa_version().startswith(b"simplicial_mi355x")
+    # the binding's struct layouts, the header and the library agree on the ABI version
+    macro = int(re.search(r"#define SIMPLICIAL_MI355X_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
+    assert lib.sa_abi_version() == macro == _native.ABI_VERSION
 
 
 def _c_layout(struct, fields):
@@ -372,3 +375,8 @@ def test_backward_workspace_reserves_dk1_partials_for_fused_shapes(dtype, hq, hk
         args.fwd.total_tokens = args.fwd.seqlen = big
         rows = (big * hq * 4 + 255) // 256 * 256
         assert lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args)) == 2 * rows
+    # a caller short of memory selects the separate dk1 pass: no partials reserved
+    args.fwd.total_tokens = args.fwd.seqlen = tokens
+    args.fwd.flags = _native.SA_FLAG_SEPARATE_DK1
+    rows = (tokens * hq * 4 + 255) // 256 * 256
+    assert lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args)) == 2 * rows + dkv2

@@ -214,8 +214,8 @@ def test_int64_metadata_and_lse(cuda):
 def test_c5_decode_config(cuda):
     """64 sequences, HQ32/HKV8, D128, w1=512 (long) w2=32 (short), page 64.
 
-    Checked against the paged oracle on a subset of tokens; two calls with
-    the same split count are bit-identical."""
+    Every one of the 64 tokens is checked against the paged oracle; two calls
+    with the same split count are bit-identical."""
     from archlab_amd.workloads import C5, paged_inputs
     paged, plan = _paged()
     inp = paged_inputs(C5, device=cuda)
@@ -226,14 +226,49 @@ def test_c5_decode_config(cuda):
     assert torch.equal(out, again) and torch.equal(lse, lse2)
     name, splits, _ = plan(*args, **kw)
     assert name == "mfma"
-    pick = [0, 1, 17, 40, 63]
     sub = [inp[k] for k in ("short_cache", "long_cache")]
-    ref_o, ref_l = O.paged_reference(inp["q"][pick].cpu(), _gather_only(sub[0]), _gather_only(sub[1]), inp["block_table"].cpu(), inp["token_seq"][pick].cpu(),
-                                     inp["token_pos"][pick].cpu(), short_window=C5.w2, long_window=C5.w1,
-                                     scale=1.0, return_lse=True)
-    assert_out_close(out[pick], ref_o, torch.bfloat16)
-    assert_lse_close(lse[pick], ref_l, torch.bfloat16)
-    print(f"[{name}] C5 splits={splits}", flush=True)
+    ref_o, ref_l = O.paged_reference(inp["q"].cpu(), _gather_only(sub[0]), _gather_only(sub[1]),
+                                     inp["block_table"].cpu(), inp["token_seq"].cpu(), inp["token_pos"].cpu(),
+                                     short_window=C5.w2, long_window=C5.w1, scale=1.0, return_lse=True)
+    err = assert_out_close(out, ref_o, torch.bfloat16)
+    rel = assert_lse_close(lse, ref_l, torch.bfloat16)
+    print(f"[{name}] C5 splits={splits}: all 64 tokens, out max-abs {err:.2e}, lse rel {rel:.2e}", flush=True)
+
+
+def test_physical_page_placement_is_bit_exact(cuda):
+    """Page-table handling is bit-exact: the same logical rows placed in
+    contiguous pages (identity table) or scattered over a shuffled pool give
+    identical bits, on both kernels, with one table or a table per axis."""
+    paged, plan = _paged()
+    dim, heads, kv_heads, bs, lengths = 128, 8, 2, 16, [70, 129, 33]
+    for qdtype, cdtype in ((torch.bfloat16, torch.bfloat16), (torch.float32, torch.bfloat16),
+                           (torch.float32, torch.float32)):
+        (short, long), table, _ = paged_batch(lengths, kv_heads, dim, bs, cdtype, seed=31, device=cuda)
+        # the same logical rows in identity order: page i of sequence s at 1 + sum(pages before s) + i
+        ident = torch.zeros_like(table)
+        nxt = 1
+        for s, n in enumerate(lengths):
+            pages = -(-n // bs)
+            ident[s, :pages] = torch.arange(nxt, nxt + pages, dtype=table.dtype, device=cuda)
+            nxt += pages
+        flat_short, flat_long = torch.zeros_like(short), torch.zeros_like(long)
+        for s, n in enumerate(lengths):
+            pages = -(-n // bs)
+            for src, dst in ((short, flat_short), (long, flat_long)):
+                dst[:, ident[s, :pages].long()] = src[:, table[s, :pages].long()]
+        g = torch.Generator().manual_seed(32)
+        tokens = [(0, 69), (1, 128), (2, 32), (1, 5), (0, 0)]
+        q = torch.randn(len(tokens), heads, dim, generator=g).to(qdtype).to(cuda)
+        seq = torch.tensor([t[0] for t in tokens], dtype=torch.int32, device=cuda)
+        pos = torch.tensor([t[1] for t in tokens], dtype=torch.int32, device=cuda)
+        kw = dict(short_window=24, long_window=100, scale=dim ** -0.5, return_lse=True)
+        o1, l1 = paged(q, short, long, table, seq, pos, **kw)
+        o2, l2 = paged(q, flat_short, flat_long, ident, seq, pos, **kw)
+        o3, l3 = paged(q, flat_short, long, ident, seq, pos, long_block_table=table, **kw)
+        assert torch.equal(o1, o2) and torch.equal(l1, l2)
+        assert torch.equal(o1, o3) and torch.equal(l1, l3)
+        name = plan(q, short, long, table, seq, pos, short_window=24, long_window=100)[0]
+        print(f"[{name}] q {qdtype} caches {cdtype}: placement-invariant", flush=True)
 
 
 class _gather_only:
@@ -349,6 +384,36 @@ def test_mixed_index_and_cache_dtypes(cuda):
     mix = paged(q.float(), short, long.float(), table, seq, pos, **kw)
     torch.testing.assert_close(mix, ref, rtol=0, atol=0)
     assert plan(q.float(), short, long.float(), table, seq, pos, **kw)[0] == "generic"
+
+
+@pytest.mark.parametrize("qdtype,tol", [(torch.bfloat16, 3e-2), (torch.float32, 2e-4)])
+@pytest.mark.parametrize("short_dtype,long_dtype", [(torch.float16, torch.float16), (torch.float16, torch.bfloat16),
+                                                    (torch.bfloat16, torch.float16), (torch.float32, torch.float16)])
+def test_fp16_caches(cuda, qdtype, tol, short_dtype, long_dtype):
+    """fp16 short and long caches, alone or mixed with bf16 / fp32 ones, as the
+    reference's paged loads accept them (simplicial_paged.py:42-52): against
+    the paged oracle on the cache values (bf16 query: the reference rounds
+    q ⊙ k1, k2 and v2 to bf16, within the bf16 tolerance; fp32 query: 2e-4)."""
+    paged, plan = _paged()
+    dim, heads, kv_heads, bs, lengths = 64, 8, 2, 16, [23, 70]
+    (short, long), table, _ = paged_batch(lengths, kv_heads, dim, bs, torch.float32, seed=41, device="cpu")
+    short, long = short.to(short_dtype), long.to(long_dtype)
+    g = torch.Generator().manual_seed(42)
+    tokens = [(0, 22), (1, 69), (1, 40), (0, 3), (1, 0)]
+    q = (torch.randn(len(tokens), heads, dim, generator=g) * dim ** -0.5).to(qdtype)
+    seq = torch.tensor([t[0] for t in tokens], dtype=torch.int32)
+    pos = torch.tensor([t[1] for t in tokens], dtype=torch.int32)
+    kw = dict(short_window=8, long_window=40, scale=1.0)
+    out, lse = paged(q.to(cuda), short.to(cuda), long.to(cuda), table.to(cuda), seq.to(cuda), pos.to(cuda),
+                     return_lse=True, **kw)
+    ref_o, ref_l = O.paged_reference(q.float(), short.float(), long.float(), table, seq, pos, return_lse=True, **kw)
+    err = (out.cpu() - ref_o).abs().max().item()
+    torch.testing.assert_close(out.cpu(), ref_o, rtol=tol, atol=tol)
+    torch.testing.assert_close(lse.cpu(), ref_l, rtol=tol, atol=tol)
+    name = plan(q.to(cuda), short.to(cuda), long.to(cuda), table.to(cuda), seq.to(cuda), pos.to(cuda),
+                short_window=8, long_window=40)[0]
+    print(f"[{name}] q {qdtype} short {short_dtype} long {long_dtype}: max-abs {err:.2e}", flush=True)
+    assert name == "generic"
 
 
 @pytest.mark.parametrize("dim", [64, 128])

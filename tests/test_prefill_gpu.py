@@ -25,6 +25,11 @@ def _api():
     return simplicial_attention, simplicial_varlen_attention, prefill_kernel_name
 
 
+# (max relative LSE error against the fp32 oracle at positions with < 64
+# pairs, case) of every bf16 check in this module, for the closing report
+_FEW_PAIR_LSE = []
+
+
 def _check(cuda, b, n, hq, hk, d, ws, wl, dtype, seed=0, positions=None, scale=1.0, sigma=1.0, kernel="auto",
            dv=None, mutate=None):
     """Kernel vs oracle on seeded inputs; returns (out, lse) at ``positions``.
@@ -59,16 +64,20 @@ def _check(cuda, b, n, hq, hk, d, ws, wl, dtype, seed=0, positions=None, scale=1
         print(f"{label}: out {e1:.2e} lse {e2:.2e}", flush=True)
         return out, lse
     full = [i for i, p in enumerate(pos) if min(p + 1, ws) * min(p + 1, wl) >= 64]
+    few = [i for i, p in enumerate(pos) if min(p + 1, ws) * min(p + 1, wl) < 64]
     ro, rl = O.kernel_rounding_reference(*x, ws, wl, scale=scale, query_positions=pos)
     rel = lambda a, e: ((a.float() - e.float()).abs() / e.float().abs().clamp_min(1.0)).max().item()  # noqa: E731
     stats = {
         "out": (out.float() - ref_o).abs().max().item(),
         "lse_full": rel(lse[:, full], ref_l[:, full]) if full else 0.0,
+        "lse_few": rel(lse[:, few], ref_l[:, few]) if few else 0.0,
         "lse_all": rel(lse, ref_l),
         "r_out": (out.float() - ro.float()).abs().max().item(),
         "r_lse": rel(lse, rl),
     }
     print(label + ": " + " ".join(f"{k} {v:.2e}" for k, v in stats.items()), flush=True)
+    if few:
+        _FEW_PAIR_LSE.append((stats["lse_few"], label))
     assert_out_close(out, ref_o, dtype)
     if full:
         assert_lse_close(lse[:, full], ref_l[:, full], dtype)
@@ -404,3 +413,15 @@ def test_contract_errors(cuda):
     assert attn(x[0].float().requires_grad_(), *(t.float() for t in x[1:]), 2, 4).grad_fn is not None
     with pytest.raises(ValueError, match="MFMA kernel does not cover"):
         attn(*(t.float()[..., :32] for t in x), 2, 4, kernel="mfma")  # fp32 at D = 32
+
+
+def test_zz_report_few_pair_lse_error(cuda):
+    """The measured maximum of the LSE error at positions whose windows hold
+    fewer than 64 pairs (bound 1e-2 there, 1e-3 elsewhere), over every bf16
+    check of this module that ran before this test."""
+    if not _FEW_PAIR_LSE:
+        pytest.skip("no bf16 check with few-pair positions ran in this session")
+    worst, case = max(_FEW_PAIR_LSE)
+    print(f"few-pair positions: max lse rel error {worst:.3e} (bound 1.0e-02) over {len(_FEW_PAIR_LSE)} checks; "
+          f"worst in {case}", flush=True)
+    assert worst <= 1e-2
