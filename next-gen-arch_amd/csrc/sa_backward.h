@@ -39,6 +39,12 @@ struct BwdParams {
   // passes run as two launches and carry the first one's fp32 sums here,
   // [tokens][hk][D] then [tokens][hk][DV]; null: the portable dk2 / dv2 pass
   float* dkv2p;
+  // fp32 inputs on the matrix cores: k2 and v2 as rows of [hi: D | lo: D]
+  // bf16 terms ([tokens][hk][2 D], split_hilo in the workspace); q, k1, v1,
+  // dout stay fp32 and their products are split in the kernels
+  const bf16* k2s;
+  const bf16* v2s;
+  int f32;
 };
 
 // Queries per dq workgroup (4 waves: NQ queries x NH = 4 / NQ heads of one KV

@@ -528,6 +528,23 @@ static size_t dkv2_lds(int d, int dv) {
 static size_t bwd_row_bytes(const sa_prefill_bwd_args* a) {
   return ((size_t)a->fwd.total_tokens * a->fwd.heads_q * sizeof(float) + 255) & ~(size_t)255;
 }
+// fp32 inputs on the matrix cores: equal widths of 64 or 128 and one 32-row
+// group of short keys (the dq pass; the other passes fall back to the
+// portable kernels where their fp32 forms do not apply), 16-byte rows.
+static bool f32_mfma_shape(const sa_prefill_args& f) {
+  if (f.dtype != SA_DTYPE_F32 || (f.flags & SA_FLAG_FORCE_GENERIC)) return false;
+  if (f.head_dim != f.value_dim || (f.head_dim != 64 && f.head_dim != 128) || f.short_window > 32) return false;
+  const int64_t st[] = {f.q_stride_t, f.q_stride_h, f.k_stride_t, f.k_stride_h, f.v_stride_t, f.v_stride_h};
+  for (int64_t x : st)
+    if (x % 4) return false;
+  return true;
+}
+// hi/lo rows of k2 and v2 for fp32 inputs on the matrix cores: [tokens][hk][2 D] bf16 each
+static size_t f32_split_bytes(const sa_prefill_bwd_args* a) {
+  const sa_prefill_args& f = a->fwd;
+  if (!f32_mfma_shape(f)) return 0;
+  return ((size_t)f.total_tokens * f.heads_kv * f.head_dim * 4 + 255) / 256 * 256;
+}
 // Shapes whose dk1 may come from the dq pass (bwd_dk1_fused_ok adds the
 // stride and alignment conditions): the partials' workspace is reserved for
 // every such call.
@@ -535,8 +552,10 @@ static bool dk1_fused_shape(const sa_prefill_bwd_args* a) {
   const sa_prefill_args& f = a->fwd;
   const bool narrow = (f.head_dim == 64 || f.head_dim == 128) && (f.value_dim == 64 || f.value_dim == 128);
   const bool wide = f.head_dim == 256 && (f.value_dim == 128 || f.value_dim == 256);
-  return f.dtype == SA_DTYPE_BF16 && !(f.flags & (SA_FLAG_FORCE_GENERIC | SA_FLAG_SEPARATE_DK1)) &&
-         (narrow || wide) && f.short_window <= 32 && f.heads_kv > 0;
+  if (f.flags & SA_FLAG_SEPARATE_DK1) return false;
+  if (f.dtype == SA_DTYPE_F32) return f32_mfma_shape(f) && f.heads_kv > 0;
+  return f.dtype == SA_DTYPE_BF16 && !(f.flags & SA_FLAG_FORCE_GENERIC) && (narrow || wide) &&
+         f.short_window <= 32 && f.heads_kv > 0;
 }
 // The partials take 16-17.5x the bytes of q; past kDk1PartialCap (or with
 // SA_FLAG_SEPARATE_DK1, for callers short of memory) the separate dk1 pass
@@ -565,7 +584,7 @@ static size_t dkv2_partial_bytes(const sa_prefill_bwd_args* a) {
   return ((size_t)f.total_tokens * f.heads_kv * (f.head_dim + f.value_dim) * sizeof(float) + 255) & ~(size_t)255;
 }
 size_t prefill_bwd_workspace_bytes(const sa_prefill_bwd_args* a) {
-  return 2 * bwd_row_bytes(a) + dk1_partial_bytes(a) + dkv2_partial_bytes(a);
+  return 2 * bwd_row_bytes(a) + dk1_partial_bytes(a) + dkv2_partial_bytes(a) + 2 * f32_split_bytes(a);
 }
 
 template <typename T>
@@ -665,7 +684,22 @@ hipError_t launch_prefill_bwd(const sa_prefill_bwd_args* a, void* ws, hipStream_
   p.d = f.head_dim;
   p.dv = f.value_dim;
   p.scale = f.scale;
-  p.mfma = f.dtype == SA_DTYPE_BF16 && !(f.flags & SA_FLAG_FORCE_GENERIC);
+  p.f32 = f.dtype == SA_DTYPE_F32;
+  p.mfma = (f.dtype == SA_DTYPE_BF16 && !(f.flags & SA_FLAG_FORCE_GENERIC)) || f32_mfma_shape(f);
+  if (size_t sb = f32_split_bytes(a)) {
+    // k2 and v2 as hi/lo bf16 rows for the fp32 matrix-core passes
+    char* base = (char*)ws + 2 * bwd_row_bytes(a) + dk1_partial_bytes(a) + dkv2_partial_bytes(a);
+    bf16* k2s = (bf16*)base;
+    bf16* v2s = (bf16*)(base + sb);
+    hipError_t e = launch_split_hilo((const float*)f.k2, f.k_stride_t, f.k_stride_h, f.total_tokens, f.heads_kv,
+                                     f.head_dim, k2s, stream);
+    if (e == hipSuccess)
+      e = launch_split_hilo((const float*)f.v2, f.v_stride_t, f.v_stride_h, f.total_tokens, f.heads_kv,
+                            f.value_dim, v2s, stream);
+    if (e != hipSuccess) return e;
+    p.k2s = k2s;
+    p.v2s = v2s;
+  }
   if (dk1_partial_bytes(a) && bwd_dk1_fused_ok(p)) p.dk1p = (float*)((char*)ws + 2 * bwd_row_bytes(a));
   if (dkv2_partial_bytes(a)) p.dkv2p = (float*)((char*)ws + 2 * bwd_row_bytes(a) + dk1_partial_bytes(a));
   if (f.dtype == SA_DTYPE_F32) return launch_bwd_t<float>(p, stream);

@@ -143,6 +143,101 @@ struct BwdOps {
     pb0 = __builtin_bit_cast(bf16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
     pb1 = __builtin_bit_cast(bf16x8, u32x4{pk[4], pk[5], pk[6], pk[7]});
   }
+
+  // ---- fp32 inputs: every operand as hi + lo bf16 terms (split_bf16), each
+  // product on three term pairs (hi·hi + hi·lo + lo·hi), as the forward's
+  // fp32 path; the reference computes these dots with tf32x3
+  // (simplicial_kernels.py:75-101).  Tile rows hold [hi: D | lo: D].
+
+  // rows_x with hi/lo tile rows and hi (x) / lo (xl) fragments
+  template <int RS>
+  __device__ static __forceinline__ floatx16 rows_x_hl(const char* tile, int row0, int lane, const bf16x8* x,
+                                                       const bf16x8* xl) {
+    const int n = lane & 31, half = lane >> 5;
+    const char* kp = tile + (row0 + n) * RS + 16 * half;
+    floatx16 c = floatx16{};
+    bf16x8 fh = *(const bf16x8*)kp, fl = *(const bf16x8*)(kp + 2 * D);
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) {
+      bf16x8 nh, nl;
+      if (t + 1 < D / 16) {
+        nh = *(const bf16x8*)(kp + 32 * (t + 1));
+        nl = *(const bf16x8*)(kp + 2 * D + 32 * (t + 1));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      c = mfma32x32x16(fh, x[t], c);
+      c = mfma32x32x16(fh, xl[t], c);
+      c = mfma32x32x16(fl, x[t], c);
+      __builtin_amdgcn_sched_barrier(0);
+      fh = nh;
+      fl = nl;
+    }
+    return c;
+  }
+
+  // tr_acc with hi/lo tile rows and the B operand as hi (pb0, pb1) and lo
+  // (pl0, pl1) terms
+  template <int RS>
+  __device__ static __forceinline__ void tr_acc_hl(floatx16* acc, const char* tile, int row0, int lane,
+                                                   const bf16x8& pb0, const bf16x8& pb1, const bf16x8& pl0,
+                                                   const bf16x8& pl1) {
+    const int half = lane >> 5, g16 = (lane >> 4) & 1, i16 = lane & 15;
+    const int e_src = i16 >> 2, q_src = i16 & 3;
+    const uint32_t vp = lds_addr(tile + (row0 + 4 * half + e_src) * RS + 32 * g16 + 8 * q_src);
+    constexpr int kSteps = 2 * (D / 32);
+    static_for<0, kSteps>([&](auto st) {
+      constexpr int s = decltype(st)::value;
+      shortx4 h1, h2, l1, l2;
+      RB::template vread<RS, s>(vp, h1, h2);
+      RB::template vread<RS, s, 2 * D>(vp, l1, l2);
+      lds_wait(h1, h2);
+      lds_wait(l1, l2);
+      const bf16x8 vh = __builtin_bit_cast(bf16x8, shortx8{h1[0], h1[1], h1[2], h1[3], h2[0], h2[1], h2[2], h2[3]});
+      const bf16x8 vl = __builtin_bit_cast(bf16x8, shortx8{l1[0], l1[1], l1[2], l1[3], l2[0], l2[1], l2[2], l2[3]});
+      const bf16x8& bh = s / (D / 32) == 0 ? pb0 : pb1;
+      const bf16x8& bl = s / (D / 32) == 0 ? pl0 : pl1;
+      __builtin_amdgcn_sched_barrier(0);
+      acc[s % (D / 32)] = mfma32x32x16(vh, bh, acc[s % (D / 32)]);
+      acc[s % (D / 32)] = mfma32x32x16(vh, bl, acc[s % (D / 32)]);
+      acc[s % (D / 32)] = mfma32x32x16(vl, bh, acc[s % (D / 32)]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  }
+
+  // pack_c with the low-order terms: x = hi + lo to 2^-17 relative
+  __device__ static __forceinline__ void pack_c_hl(const float* x, bf16x8& pb0, bf16x8& pb1, bf16x8& pl0,
+                                                   bf16x8& pl1) {
+    uint32_t ph[8], pl[8];
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) pack_bf16_split(x[r], x[r + 1], ph[r >> 1], pl[r >> 1]);
+    pb0 = __builtin_bit_cast(bf16x8, u32x4{ph[0], ph[1], ph[2], ph[3]});
+    pb1 = __builtin_bit_cast(bf16x8, u32x4{ph[4], ph[5], ph[6], ph[7]});
+    pl0 = __builtin_bit_cast(bf16x8, u32x4{pl[0], pl[1], pl[2], pl[3]});
+    pl1 = __builtin_bit_cast(bf16x8, u32x4{pl[4], pl[5], pl[6], pl[7]});
+  }
+
+  // A^T fragments (hi a, lo al) of rows x ⊙ y from fp32 rows in LDS: lane
+  // (n, half) holds d = 16t + 8 half .. +7 of its row; zero where !valid
+  __device__ static __forceinline__ void form_hl_lds(const char* xrow, const char* yrow, bool valid, int half,
+                                                     bf16x8* a, bf16x8* al) {
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) {
+      const int d0 = 16 * t + 8 * half;
+      const floatx4 x0 = *(const floatx4*)(xrow + 4 * d0), x1 = *(const floatx4*)(xrow + 4 * d0 + 16);
+      const floatx4 y0 = *(const floatx4*)(yrow + 4 * d0), y1 = *(const floatx4*)(yrow + 4 * d0 + 16);
+      bf16x8 h, l;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float v = valid ? (u < 4 ? x0[u] * y0[u] : x1[u - 4] * y1[u - 4]) : 0.f;
+        bf16 vh, vl;
+        split_bf16(v, vh, vl);
+        h[u] = vh;
+        l[u] = vl;
+      }
+      a[t] = h;
+      al[t] = l;
+    }
+  }
 };
 
 struct BwdGeo {
@@ -160,12 +255,19 @@ struct BwdGeo {
 // FUSE (one row group): the pass also writes the block's dk1 partial, Σ over
 // its NQ queries and NH heads of dA_{t,j} ⊙ q_{t,h} for the short keys
 // j = t0 - 31 .. t0 + NQ - 1 (the dk1 pass's G_{t,j} is the same dA_{t,j}).
-template <int DK, int DV, int NQ, int NH, int P, bool FUSE = false>
-__global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dq_mfma_kernel(BwdParams p, BwdGeo geo) {
+// F32: fp32 inputs (DK == DV <= 128): K2 / V2 tiles from the hi/lo rows
+// (p.k2s, p.v2s), the short slot and the q / dout rows hold fp32 rows (the
+// same bytes as a hi/lo row), A and B are split from fp32 products, and every
+// product runs on three term pairs; dq (and dk1) in fp32.
+template <int DK, int DV, int NQ, int NH, int P, bool FUSE = false, bool F32 = false>
+__global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_dq_mfma_kernel(BwdParams p,
+                                                                                            BwdGeo geo) {
   static_assert(NQ * NH == 4, "4 waves per block");
+  static_assert(!F32 || (DK == DV && DK <= 128), "fp32 inputs: equal widths up to 128");
   constexpr int NW = NQ * NH;
   constexpr int ROWS = kChunk + NQ - 1;
-  using G = TileGeom<DK, DV, ROWS, NW, 32, 32>;
+  constexpr int EW = F32 ? 2 : 1;  // bf16 units per element of an LDS row (fp32 rows, hi/lo tile rows)
+  using G = TileGeom<EW * DK, EW * DV, ROWS, NW, 32, 32>;
   using OPK = BwdOps<DK>;  // products over the score width
   using OPV = BwdOps<DV>;  // ... over the value width
   constexpr int R = P + 1;
@@ -208,12 +310,18 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dq_mfma_ke
 
   const int kb0 = t0 - p.wl + 1;  // key of tile row 0 at chunk 0
   const int last = p.tokens - 1;
-  const int64_t k_st = p.k_st, v_st = p.v_st;
-  const int64_t k_g = (int64_t)g * p.k_sh, v_g = (int64_t)g * p.v_sh;
+  // strides in bf16 units: the long-axis tiles (bf16 tensors, or the fp32
+  // inputs' hi/lo rows [tokens][hk][2 D]) and the short slot (bf16 tensors,
+  // or fp32 rows viewed as two bf16 units per element)
+  const int64_t k_st = F32 ? (int64_t)p.hk * 2 * DK : p.k_st, v_st = F32 ? (int64_t)p.hk * 2 * DV : p.v_st;
+  const int64_t k_g = F32 ? (int64_t)g * 2 * DK : (int64_t)g * p.k_sh;
+  const int64_t v_g = F32 ? (int64_t)g * 2 * DV : (int64_t)g * p.v_sh;
+  const int64_t ks_st = EW * p.k_st, vs_st = EW * p.v_st;
+  const int64_t ks_g = EW * (int64_t)g * p.k_sh, vs_g = EW * (int64_t)g * p.v_sh;
   const bf16* const k1 = (const bf16*)p.k1;
-  const bf16* const k2 = (const bf16*)p.k2;
+  const bf16* const k2 = F32 ? p.k2s : (const bf16*)p.k2;
   const bf16* const v1 = (const bf16*)p.v1;
-  const bf16* const v2 = (const bf16*)p.v2;
+  const bf16* const v2 = F32 ? p.v2s : (const bf16*)p.v2;
 
   uint32_t voff[NI];
 #pragma unroll
@@ -222,12 +330,14 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dq_mfma_ke
     G::decode(wid, k, lane, is_v, row, seg);
     voff[k] = (uint32_t)(((int64_t)row * (is_v ? v_st : k_st) + seg * 8) * 2);
   }
-  // One tile of rows kb .. kb+ROWS-1: K region from kt, V region from vt.
-  auto dma_tile = [&](char* slot, int kb_in, const bf16* kt, const bf16* vt) {
+  // One tile of rows kb .. kb+ROWS-1: K region from kt, V region from vt
+  // (row strides kst / vst, head offsets kg / vg, in bf16 units).
+  auto dma_tile = [&](char* slot, int kb_in, const bf16* kt, const bf16* vt, int64_t kst, int64_t vst, int64_t kg,
+                      int64_t vg, bool same_strides) {
     const int kb = __builtin_amdgcn_readfirstlane(kb_in);
-    if (kb >= 0 && kb + ROWS - 1 <= last) {
-      const char* kbase = (const char*)(kt + (int64_t)kb * k_st + k_g);
-      const char* vbase = (const char*)(vt + (int64_t)kb * v_st + v_g);
+    if (same_strides && kb >= 0 && kb + ROWS - 1 <= last) {
+      const char* kbase = (const char*)(kt + (int64_t)kb * kst + kg);
+      const char* vbase = (const char*)(vt + (int64_t)kb * vst + vg);
 #pragma unroll
       for (int k = 0; k < NI; ++k)
         dma16(uniform_ptr(G::instr_is_v(wid, k) ? vbase : kbase) + voff[k], G::dst(slot, wid, k));
@@ -239,12 +349,14 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dq_mfma_ke
         int is_v, row, seg;
         G::decode(wid, k, lf, is_v, row, seg);
         const int64_t key = min(max(kb + row, 0), last);
-        const bf16* src = is_v ? vt + key * v_st + v_g : kt + key * k_st + k_g;
+        const bf16* src = is_v ? vt + key * vst + vg : kt + key * kst + kg;
         dma16(src + seg * 8, G::dst(slot, wid, k));
       }
     }
   };
-  auto issue = [&](int c) { dma_tile(lds + (c % R) * G::SLOT, kb0 + kChunk * c, k2, v2); };
+  auto issue = [&](int c) {
+    dma_tile(lds + (c % R) * G::SLOT, kb0 + kChunk * c, k2, v2, k_st, v_st, k_g, v_g, true);
+  };
   // q and dout rows of the NW (query, head) pairs (wave 0; QI instructions)
   constexpr int QI = (NW * (G::RSK + G::RSV) + 1023) / 1024;
   auto dma_qd = [&]() {
@@ -258,8 +370,8 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dq_mfma_ke
         if (row >= NW || seg >= (isd ? G::kSegsV : G::kSegsK)) row = 0, seg = 0;
         const int tq = min(t0 + row / NH, last);
         const int hq = g * p.group + hs * NH + row % NH;
-        const bf16* src = isd ? (const bf16*)p.dout + (int64_t)tq * p.do_st + (int64_t)hq * p.do_sh
-                              : (const bf16*)p.q + (int64_t)tq * p.q_st + (int64_t)hq * p.q_sh;
+        const bf16* src = isd ? (const bf16*)p.dout + EW * ((int64_t)tq * p.do_st + (int64_t)hq * p.do_sh)
+                              : (const bf16*)p.q + EW * ((int64_t)tq * p.q_st + (int64_t)hq * p.q_sh);
         dma16(src + seg * 8, qslot + k * 1024);
       }
     }
@@ -275,8 +387,8 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dq_mfma_ke
   const float dpm = single ? 0.f : p.scale;
   const float dsm = single ? dl * p.scale : -delta * p.scale;
 
-  RowBlock<DK, DV> ra;  // A rows (q ⊙ k1); only the fragments are used
-  RowBlock<DV, DV> rbv;  // B rows (dout ⊙ v1)
+  RowBlock<DK, DV, F32> ra;  // A rows (q ⊙ k1); only the fragments are used
+  RowBlock<DV, DV, F32> rbv;  // B rows (dout ⊙ v1)
   float dqrun[DK / 64];
 #pragma unroll
   for (int i = 0; i < DK / 64; ++i) dqrun[i] = 0.f;
@@ -286,15 +398,21 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dq_mfma_ke
     const bool row_ok = qvalid && j >= lo1;
     const float lse2r = row_ok ? lse2 : INFINITY;  // exp2(x - inf) = 0: rows outside the window
     const int kbs = t0 - 31 - 32 * r;  // short-slot row 0
-    dma_tile(sslot, kbs, k1, v1);
+    dma_tile(sslot, kbs, k1, v1, ks_st, vs_st, ks_g, vs_g, !F32);
     if (r == 0) dma_qd();
 #pragma unroll
     for (int e = 0; e < P; ++e) issue(c0 + e);  // unconditional: static count for the wait below
     wait_vmcnt<P * NI>();
     block_barrier();
     const int srow = qo + 31 - n;  // row of key j in the short slot
-    ra.form_a_lds(sslot + srow * G::RSK, qslot + wid * G::RSK, row_ok, half, false);
-    rbv.form_a_lds(sslot + G::VOFF + srow * G::RSV, qslot + NW * G::RSK + wid * G::RSV, row_ok, half, false);
+    if constexpr (F32) {
+      OPK::form_hl_lds(sslot + srow * G::RSK, qslot + wid * G::RSK, row_ok, half, ra.a, ra.al);
+      OPV::form_hl_lds(sslot + G::VOFF + srow * G::RSV, qslot + NW * G::RSK + wid * G::RSV, row_ok, half, rbv.a,
+                       rbv.al);
+    } else {
+      ra.form_a_lds(sslot + srow * G::RSK, qslot + wid * G::RSK, row_ok, half, false);
+      rbv.form_a_lds(sslot + G::VOFF + srow * G::RSV, qslot + NW * G::RSK + wid * G::RSV, row_ok, half, false);
+    }
 
     floatx16 dA[DK / 32];
 #pragma unroll
@@ -308,8 +426,14 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dq_mfma_ke
       const int klo = active ? max(lo2 - kfirst, 0) : kChunk;
       const int khi = active ? min(t - kfirst, kChunk - 1) : -1;
       const char* slot = lds + (c % R) * G::SLOT;
-      const floatx16 s = OPK::template rows_x<G::RSK, kDqPF>(slot, qo, lane, ra.a);
-      const floatx16 dp = OPV::template rows_x<G::RSV, kDqPF>(slot + G::VOFF, qo, lane, rbv.a);
+      floatx16 s, dp;
+      if constexpr (F32) {
+        s = OPK::template rows_x_hl<G::RSK>(slot, qo, lane, ra.a, ra.al);
+        dp = OPV::template rows_x_hl<G::RSV>(slot + G::VOFF, qo, lane, rbv.a, rbv.al);
+      } else {
+        s = OPK::template rows_x<G::RSK, kDqPF>(slot, qo, lane, ra.a);
+        dp = OPV::template rows_x<G::RSV, kDqPF>(slot + G::VOFF, qo, lane, rbv.a);
+      }
       // register r holds chunk key 8*(r/4) + r%4 + 4*half of column j = this lane's row
       const int lo_h = klo - 4 * half, hi_h = khi - 4 * half;
       float ds[16];
@@ -327,8 +451,14 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dq_mfma_ke
         }
       }
       bf16x8 pb0, pb1;
-      OPK::pack_c(ds, pb0, pb1);
-      OPK::template tr_acc<G::RSK, kDqPF>(dA, slot, qo, lane, pb0, pb1);  // dA^T += K2^T · dS^T
+      if constexpr (F32) {
+        bf16x8 pl0, pl1;
+        OPK::pack_c_hl(ds, pb0, pb1, pl0, pl1);
+        OPK::template tr_acc_hl<G::RSK>(dA, slot, qo, lane, pb0, pb1, pl0, pl1);  // dA^T += K2^T · dS^T
+      } else {
+        OPK::pack_c(ds, pb0, pb1);
+        OPK::template tr_acc<G::RSK, kDqPF>(dA, slot, qo, lane, pb0, pb1);  // dA^T += K2^T · dS^T
+      }
     }
     wait_vmcnt<0>();
     block_barrier();  // ring reads done (LDS reused below)
@@ -336,14 +466,22 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dq_mfma_ke
     // dq[d] += Σ_j dA_j[d] k1_j[d] over the wave's 32 rows
     float* red = (float*)lds + wid * (64 * 36);  // [64 d][36] per wave (ring region)
     const char* k1s = sslot + srow * G::RSK;     // this lane's k1 row
-    bf16x4 kv[DK / 64][2][4];
+    floatx4 kv[DK / 64][2][4];
 #pragma unroll
     for (int sl = 0; sl < DK / 64; ++sl)
 #pragma unroll
       for (int dbl = 0; dbl < 2; ++dbl)
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4)
-          kv[sl][dbl][q4] = *(const bf16x4*)(k1s + 2 * (64 * sl + 32 * dbl + 8 * q4 + 4 * half));
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int dd = 64 * sl + 32 * dbl + 8 * q4 + 4 * half;
+          if constexpr (F32) {
+            kv[sl][dbl][q4] = *(const floatx4*)(k1s + 4 * dd);
+          } else {
+            const bf16x4 kb = *(const bf16x4*)(k1s + 2 * dd);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) kv[sl][dbl][q4][e] = (float)kb[e];
+          }
+        }
 #pragma unroll
     for (int sl = 0; sl < DK / 64; ++sl) {
 #pragma unroll
@@ -354,7 +492,7 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dq_mfma_ke
           const int dd = 32 * dbl + 8 * q4 + 4 * half;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float k = row_ok ? (float)kv[sl][dbl][q4][e] : 0.f;
+            const float k = row_ok ? kv[sl][dbl][q4][e] : 0.f;
             red[(dd + e) * 36 + n] = k * dA[db][4 * q4 + e];
           }
         }
@@ -390,10 +528,17 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dq_mfma_ke
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4) {
             const int dd = 32 * dbl + 8 * q4 + 4 * half;
-            const bf16x4 qv = *(const bf16x4*)(qrow + 2 * (64 * dh + dd));
+            floatx4 qv;
+            if constexpr (F32) {
+              qv = *(const floatx4*)(qrow + 4 * (64 * dh + dd));
+            } else {
+              const bf16x4 qb = *(const bf16x4*)(qrow + 2 * (64 * dh + dd));
+#pragma unroll
+              for (int e = 0; e < 4; ++e) qv[e] = (float)qb[e];
+            }
             floatx4 x;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) x[e] = row_ok ? (float)qv[e] * dA[2 * dh + dbl][4 * q4 + e] : 0.f;
+            for (int e = 0; e < 4; ++e) x[e] = row_ok ? qv[e] * dA[2 * dh + dbl][4 * q4 + e] : 0.f;
             *(floatx4*)(pw + dd) = x;
           }
         block_barrier();  // every wave's rows staged
@@ -415,37 +560,49 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dq_mfma_ke
   }
 
   if (qvalid) {
-    bf16* orow = (bf16*)p.dq + (int64_t)t * p.dq_st + (int64_t)h * p.dq_sh;
+    if constexpr (F32) {
+      float* orow = (float*)p.dq + (int64_t)t * p.dq_st + (int64_t)h * p.dq_sh;
 #pragma unroll
-    for (int i = 0; i < DK / 64; ++i) orow[64 * i + lane] = (bf16)dqrun[i];
+      for (int i = 0; i < DK / 64; ++i) orow[64 * i + lane] = dqrun[i];
+    } else {
+      bf16* orow = (bf16*)p.dq + (int64_t)t * p.dq_st + (int64_t)h * p.dq_sh;
+#pragma unroll
+      for (int i = 0; i < DK / 64; ++i) orow[64 * i + lane] = (bf16)dqrun[i];
+    }
   }
 }
 
-template <int DK, int DV, int NQ, int NH, bool FUSE = false>
+template <int DK, int DV, int NQ, int NH, bool FUSE = false, bool F32 = false>
 hipError_t launch_dq_t(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
-  constexpr int P = 1;  // one tile in flight: ring + short slot + q/dout rows stay <= 80 KB (2 per CU)
+  // one tile in flight: ring + short slot + q/dout rows stay <= 80 KB (2 per
+  // CU; fp32 inputs: rows twice as wide, one per CU)
+  constexpr int P = 1;
   geo.qblocks = (p.tokens + NQ - 1) / NQ;
   geo.hsub = p.group / NH;
   geo.nblocks = geo.qblocks * p.hk * geo.hsub;
   constexpr int NW = NQ * NH;
-  using G = TileGeom<DK, DV, kChunk + NQ - 1, NW, 32, 32>;
+  constexpr int EW = F32 ? 2 : 1;
+  using G = TileGeom<EW * DK, EW * DV, kChunk + NQ - 1, NW, 32, 32>;
   const size_t qslot = ((size_t)NW * (G::RSK + G::RSV) + 1023) / 1024 * 1024;
   const size_t ring = (size_t)(P + 1) * G::SLOT, red = (size_t)NW * 64 * 36 * sizeof(float);
   const size_t lds = (ring > red ? ring : red) + G::SLOT + qslot;
-  auto kern = bwd_dq_mfma_kernel<DK, DV, NQ, NH, P, FUSE>;
+  auto kern = bwd_dq_mfma_kernel<DK, DV, NQ, NH, P, FUSE, F32>;
   hipError_t e = set_lds_limit((const void*)kern, lds);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(geo.nblocks), dim3(64 * NW), lds, stream, p, geo);
   return hipGetLastError();
 }
 
-template <int DK, int DV>
+template <int DK, int DV, bool F32 = false>
 hipError_t launch_dq_d(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
   if (p.group % 4 == 0)
-    return p.dk1p ? launch_dq_t<DK, DV, 1, 4, true>(p, geo, stream) : launch_dq_t<DK, DV, 1, 4>(p, geo, stream);
+    return p.dk1p ? launch_dq_t<DK, DV, 1, 4, true, F32>(p, geo, stream)
+                  : launch_dq_t<DK, DV, 1, 4, false, F32>(p, geo, stream);
   if (p.group % 2 == 0)
-    return p.dk1p ? launch_dq_t<DK, DV, 2, 2, true>(p, geo, stream) : launch_dq_t<DK, DV, 2, 2>(p, geo, stream);
-  return p.dk1p ? launch_dq_t<DK, DV, 4, 1, true>(p, geo, stream) : launch_dq_t<DK, DV, 4, 1>(p, geo, stream);
+    return p.dk1p ? launch_dq_t<DK, DV, 2, 2, true, F32>(p, geo, stream)
+                  : launch_dq_t<DK, DV, 2, 2, false, F32>(p, geo, stream);
+  return p.dk1p ? launch_dq_t<DK, DV, 4, 1, true, F32>(p, geo, stream)
+                : launch_dq_t<DK, DV, 4, 1, false, F32>(p, geo, stream);
 }
 
 
@@ -768,10 +925,15 @@ __global__ __launch_bounds__(256) void bwd_dk1_sum_kernel(BwdParams p, int qbloc
       acc += x;
     }
   }
-  bf16x4 o;
+  const int64_t off = (int64_t)j * p.dk_st + (int64_t)g * p.dk_sh + 4 * d4;
+  if (p.f32) {
+    *(floatx4*)((float*)p.dk1 + off) = acc;
+  } else {
+    bf16x4 o;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) o[e] = (bf16)acc[e];
-  *(bf16x4*)((bf16*)p.dk1 + (int64_t)j * p.dk_st + (int64_t)g * p.dk_sh + 4 * d4) = o;
+    for (int e = 0; e < 4; ++e) o[e] = (bf16)acc[e];
+    *(bf16x4*)((bf16*)p.dk1 + off) = o;
+  }
 }
 
 
@@ -1197,9 +1359,11 @@ hipError_t launch_dkv2_d(const BwdParams& p, hipStream_t stream) {
 }
 
 // bf16, score width DK and value width DV each 64 or 128, or DK = 256 over
-// DV = 128 or 256 (the dq and dk1 / dv1 passes only), 16-byte aligned rows.
+// DV = 128 or 256 (the dq and dk1 / dv1 passes only), 16-byte aligned rows;
+// fp32 inputs (p.f32, with the hi/lo rows of k2 and v2): DK == DV in {64, 128}.
 bool bwd_mfma_ok(const BwdParams& p) {
   if (!p.mfma) return false;
+  if (p.f32 && (p.d != p.dv || (p.d != 64 && p.d != 128) || !p.k2s || !p.v2s)) return false;
   const bool narrow = (p.d == 64 || p.d == 128) && (p.dv == 64 || p.dv == 128);
   if (!narrow && !(p.d == 256 && (p.dv == 128 || p.dv == 256))) return false;
   const int64_t st[] = {p.q_st, p.q_sh, p.k_st, p.k_sh, p.v_st, p.v_sh, p.do_st, p.do_sh};
@@ -1235,11 +1399,15 @@ BwdGeo base_geo(const BwdParams& p) {
 hipError_t launch_bwd_dq_mfma(const BwdParams& p, hipStream_t stream) {
   if (!bwd_mfma_ok(p)) return hipErrorNotSupported;
   const BwdGeo geo = base_geo(p);
+  if (p.f32) {
+    if (p.ws > 32) return hipErrorNotSupported;  // fp32: one 32-row group of short keys
+    return p.d == 64 ? launch_dq_d<64, 64, true>(p, geo, stream) : launch_dq_d<128, 128, true>(p, geo, stream);
+  }
   return by_widths<true>(p, [&](auto dk, auto dv) { return launch_dq_d<decltype(dk)::value, decltype(dv)::value>(p, geo, stream); });
 }
 
 hipError_t launch_bwd_dkv1_mfma(const BwdParams& p, hipStream_t stream) {
-  if (!bwd_mfma_ok(p)) return hipErrorNotSupported;
+  if (!bwd_mfma_ok(p) || p.f32) return hipErrorNotSupported;
   const BwdGeo geo = base_geo(p);
   return by_widths<true>(p, [&](auto dk, auto dv) { return launch_dkv1_d<decltype(dk)::value, decltype(dv)::value>(p, geo, stream); });
 }
@@ -1261,7 +1429,7 @@ hipError_t launch_bwd_dk1_sum(const BwdParams& p, hipStream_t stream) {
 hipError_t launch_bwd_dkv2_mfma(const BwdParams& p, hipStream_t stream) {
   // one launch covers 64 short keys (32 at DK = 256); two launches over the fp32 partial twice that
   const int one = p.d > 128 ? 32 : 64;
-  if (!bwd_mfma_ok(p) || p.ws > 2 * one || (p.ws > one && !p.dkv2p)) return hipErrorNotSupported;
+  if (!bwd_mfma_ok(p) || p.f32 || p.ws > 2 * one || (p.ws > one && !p.dkv2p)) return hipErrorNotSupported;
   return by_widths<true>(p, [&](auto dk, auto dv) { return launch_dkv2_d<decltype(dk)::value, decltype(dv)::value>(p, stream); });
 }
 

@@ -27,6 +27,10 @@ struct GenericPrefillParams {
 hipError_t launch_prefill_mfma(const sa_prefill_args* a, hipStream_t stream);
 size_t prefill_f32_workspace_bytes(const sa_prefill_args* a);
 hipError_t launch_prefill_generic(const sa_prefill_args* a, hipStream_t stream);
+// fp32 rows [tokens][heads][d] (element strides st_t, st_h) -> bf16 rows
+// [tokens][heads][hi: d | lo: d], hi + lo = x to 2^-17 relative
+hipError_t launch_split_hilo(const float* src, int64_t st_t, int64_t st_h, int64_t tokens, int heads, int d,
+                             __bf16* dst, hipStream_t stream);
 
 // Paged: number of split partials per (token, head) and the launch itself.
 int paged_mfma_supported(const sa_paged_args* a);

@@ -487,6 +487,15 @@ static hipError_t dispatch_prefill_mfma_f32(const PrefillParams& p, hipStream_t 
   return launch_prefill_mfma<D, D, 4, 1, true>(p, stream);
 }
 
+hipError_t launch_split_hilo(const float* src, int64_t st_t, int64_t st_h, int64_t tokens, int heads, int d,
+                             bf16* dst, hipStream_t stream) {
+  const int64_t rows = tokens * heads;
+  if (rows == 0) return hipSuccess;
+  const unsigned blocks = (unsigned)((rows * (d / 4) + 255) / 256);
+  hipLaunchKernelGGL(split_hilo_kernel, dim3(blocks), dim3(256), 0, stream, src, st_t, st_h, rows, heads, d, dst);
+  return hipGetLastError();
+}
+
 size_t prefill_f32_workspace_bytes(const sa_prefill_args* a) {
   // k2, v2 and v1 as rows of hi and lo bf16 terms: 4 bytes per element each
   const size_t e = (size_t)a->total_tokens * a->heads_kv * a->head_dim;

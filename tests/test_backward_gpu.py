@@ -250,6 +250,45 @@ def test_backward_bf16_separate_dk1_when_partials_do_not_fit(cuda, monkeypatch):
     assert len(refused) == 2, refused  # one refused partials workspace per call, then the small one
 
 
+# ---- fp32 inputs on the matrix cores: every operand as hi + lo bf16 terms,
+# each product on three term pairs (D == DV in {64, 128}, short window <= 32;
+# the reference's DeepSeek-V4.1 adapter sends fp32, deepseek_v41_adapter.py:136-144)
+
+@pytest.mark.parametrize("b,n,hq,hk,d,ws,wl", [(1, 300, 8, 2, 128, 32, 256), (2, 70, 3, 1, 64, 20, 40),
+                                               (1, 150, 4, 4, 128, 32, 96), (2, 61, 2, 2, 64, 5, 40),
+                                               (1, 90, 3, 1, 64, 1, 1), (1, 77, 6, 2, 128, 7, 33)])
+def test_backward_fp32_matrix_cores(cuda, b, n, hq, hk, d, ws, wl):
+    _run(cuda, b, n, hq, hk, d, ws, wl, torch.float32, seed=n + ws)
+
+
+def test_backward_fp32_matrix_cores_varlen_lse_and_repeatable(cuda):
+    """Packed sequences and an LSE gradient at fp32 on the matrix cores; the
+    result repeats bit for bit and differs from the portable kernels' (a
+    different summation), both within 1e-4 of the fp64 oracle."""
+    from archlab_amd import simplicial_varlen_attention
+    lengths = [1, 45, 3, 80, 6]
+    t = sum(lengths)
+    x = [v[0] for v in rand_inputs(1, t, 8, 2, 128, seed=29, dtype=torch.float32)]
+    g = torch.Generator().manual_seed(30)
+    dout = torch.randn(t, 8, 128, generator=g)
+    dl = torch.randn(t, 8, generator=g)
+    cu = torch.tensor([0, 1, 46, 49, 129, 135], dtype=torch.int32)
+    runs = {}
+    for kernel in ("auto", "auto", "generic"):
+        xd = [v.to(cuda).requires_grad_(True) for v in x]
+        out, lse = simplicial_varlen_attention(*xd, cu.to(cuda), 32, 50, return_lse=True, kernel=kernel)
+        ((out * dout.to(cuda)).sum() + (lse * dl.to(cuda)).sum()).backward()
+        runs.setdefault(kernel, []).append([v.grad.clone() for v in xd])
+    xs = [v.double().requires_grad_(True) for v in x]
+    o, l = O.varlen_reference(*xs, cu, 32, 50, scale=128 ** -0.5, return_lse=True)
+    ((o * dout.double()).sum() + (l * dl.double()).sum()).backward()
+    ref = [v.grad.float() for v in xs]
+    _assert_grads(runs["auto"][0], ref, torch.float32, "varlen fp32 matrix cores + dlse")
+    _assert_grads(runs["generic"][0], ref, torch.float32, "varlen fp32 portable + dlse")
+    assert all(torch.equal(a, b) for a, b in zip(*runs["auto"]))
+    assert not all(torch.equal(a, b) for a, b in zip(runs["auto"][0], runs["generic"][0]))
+
+
 # ---- dk2 / dv2 on the matrix cores with short windows of 33-64 (two 32-row
 # groups of short keys per step) ----------------------------------------------------
 
