@@ -617,15 +617,21 @@ hipError_t launch_dq_d(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
 // MODE 1: dk1 only (G), MODE 2: dv1 only (O''), in two launches: one
 // accumulator set (and, for dv1, neither the B rows nor dP) fits two waves
 // per SIMD; the S recomputation is paid twice.
-template <int DK, int DV, int NQ, int NH, int P, int MODE>
-__global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dkv1_mfma_kernel(BwdParams p, BwdGeo geo) {
+// F32: fp32 inputs (DK == DV <= 128), as in the dq pass: K2 / V2 tiles from
+// the hi/lo rows, fp32 q / dout / k1 / v1 rows in LDS, products split into
+// hi/lo terms, three term pairs per product, fp32 output.
+template <int DK, int DV, int NQ, int NH, int P, int MODE, bool F32 = false>
+__global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_dkv1_mfma_kernel(BwdParams p,
+                                                                                             BwdGeo geo) {
   static_assert(NQ == 4 && NH == 1, "4 keys per block, one head at a time");
+  static_assert(!F32 || (DK == DV && DK <= 128), "fp32 inputs: equal widths up to 128");
   constexpr bool kDK = MODE == 1, kDV = MODE == 2;
   static_assert(kDK || kDV, "one output per launch");
   constexpr int XW = kDK ? DK : DV;  // width of the gradient accumulated
   constexpr int NW = NQ * NH;
   constexpr int ROWS = kChunk + NQ - 1;
-  using G = TileGeom<DK, DV, ROWS, NW, 32, 32>;
+  constexpr int EW = F32 ? 2 : 1;  // bf16 units per element of an LDS row
+  using G = TileGeom<EW * DK, EW * DV, ROWS, NW, 32, 32>;
   using OPK = BwdOps<DK>;
   using OPV = BwdOps<DV>;
   constexpr int R = P + 1;
@@ -665,10 +671,12 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dkv1_mfma_
   }
   send = __builtin_amdgcn_readfirstlane(max(send, jc + 1));
 
-  const int64_t k_st = p.k_st, v_st = p.v_st;
-  const int64_t k_g = (int64_t)g * p.k_sh, v_g = (int64_t)g * p.v_sh;
-  const bf16* const k2 = (const bf16*)p.k2;
-  const bf16* const v2 = (const bf16*)p.v2;
+  // tile strides in bf16 units (fp32 inputs: the hi/lo rows [tokens][hk][2 D])
+  const int64_t k_st = F32 ? (int64_t)p.hk * 2 * DK : p.k_st, v_st = F32 ? (int64_t)p.hk * 2 * DV : p.v_st;
+  const int64_t k_g = F32 ? (int64_t)g * 2 * DK : (int64_t)g * p.k_sh;
+  const int64_t v_g = F32 ? (int64_t)g * 2 * DV : (int64_t)g * p.v_sh;
+  const bf16* const k2 = F32 ? p.k2s : (const bf16*)p.k2;
+  const bf16* const v2 = F32 ? p.v2s : (const bf16*)p.v2;
 
   uint32_t koff[NI];  // this lane's byte offsets in a K2/V2 tile
 #pragma unroll
@@ -713,8 +721,8 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dkv1_mfma_
         int row = bb / rs, seg = (bb % rs) >> 4;
         if (row >= NW || seg >= (isv ? G::kSegsV : G::kSegsK)) row = 0, seg = 0;
         const int jr = min(j0 + row / NH, last);
-        const bf16* src = isv ? (const bf16*)p.v1 + (int64_t)jr * v_st + v_g
-                              : (const bf16*)p.k1 + (int64_t)jr * k_st + k_g;
+        const bf16* src = isv ? (const bf16*)p.v1 + EW * ((int64_t)jr * p.v_st + (int64_t)g * p.v_sh)
+                              : (const bf16*)p.k1 + EW * ((int64_t)jr * p.k_st + (int64_t)g * p.k_sh);
         dma16(src + seg * 8, kslot + k * 1024);
       }
     }
@@ -724,8 +732,8 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dkv1_mfma_
   float xrun[XW / 64];  // dk1 (MODE 1) or dv1 (MODE 2) of this wave's key, d = 64*i + lane
 #pragma unroll
   for (int i = 0; i < XW / 64; ++i) xrun[i] = 0.f;
-  RowBlock<DK, DV> ra;  // A rows (q_t ⊙ k1_j)
-  RowBlock<DV, DV> rbv;  // B rows (dout_t ⊙ v1_j)
+  RowBlock<DK, DV, F32> ra;  // A rows (q_t ⊙ k1_j)
+  RowBlock<DV, DV, F32> rbv;  // B rows (dout_t ⊙ v1_j)
   const int nc = (p.wl + 2 * kChunk - 2) / kChunk;  // chunks over wl + 31 keys
   dma_kv();
   bool first = true;
@@ -738,7 +746,7 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dkv1_mfma_
     for (int k = 0; k < NI; ++k) {
       int is_v, row, seg;
       G::decode(wid, k, lane, is_v, row, seg);
-      roff[k] = (uint32_t)(((int64_t)row * (is_v ? p.do_st : p.q_st) + seg * 8) * 2);
+      roff[k] = (uint32_t)(((int64_t)row * EW * (is_v ? p.do_st : p.q_st) + seg * 8) * 2);
     }
     for (int r = 0; r < geo.nr; ++r) {
       const int t = j + 32 * r + n;  // this lane's row (query)
@@ -754,8 +762,8 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dkv1_mfma_
       const int tb0 = j0 + 32 * r;             // query of row-slot row 0
       if (!first) block_barrier();  // the previous pass's epilogue reads of the LDS are done
       first = false;
-      dma_rows(rslot, tb0, (const bf16*)p.q, p.q_st, (int64_t)h * p.q_sh, (const bf16*)p.dout, p.do_st,
-               (int64_t)h * p.do_sh, roff);
+      dma_rows(rslot, tb0, (const bf16*)p.q, EW * p.q_st, EW * (int64_t)h * p.q_sh, (const bf16*)p.dout,
+               EW * p.do_st, EW * (int64_t)h * p.do_sh, roff);
       auto issue = [&](int c) {
         dma_rows(lds + (c % R) * G::SLOT, kb0 + kChunk * c, k2, k_st, k_g, v2, v_st, v_g, koff);
       };
@@ -765,8 +773,15 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dkv1_mfma_
       block_barrier();
       const int srow = qo + n;  // row of query t in the row slot
       // kslot row w holds the k1 (v1: row NW + w) row of key j0 + w / NH, i.e. this wave's key
-      ra.form_a_lds(rslot + srow * G::RSK, kslot + wid * G::RSK, row_ok, half, false);
-      if constexpr (kDK) rbv.form_a_lds(rslot + G::VOFF + srow * G::RSV, kslot + NW * G::RSK + wid * G::RSV, row_ok, half, false);
+      if constexpr (F32) {
+        OPK::form_hl_lds(rslot + srow * G::RSK, kslot + wid * G::RSK, row_ok, half, ra.a, ra.al);
+        if constexpr (kDK)
+          OPV::form_hl_lds(rslot + G::VOFF + srow * G::RSV, kslot + NW * G::RSK + wid * G::RSV, row_ok, half,
+                           rbv.a, rbv.al);
+      } else {
+        ra.form_a_lds(rslot + srow * G::RSK, kslot + wid * G::RSK, row_ok, half, false);
+        if constexpr (kDK) rbv.form_a_lds(rslot + G::VOFF + srow * G::RSV, kslot + NW * G::RSK + wid * G::RSV, row_ok, half, false);
+      }
 
       floatx16 acc[XW / 32];  // G^T (MODE 1) or O''^T (MODE 2)
 #pragma unroll
@@ -782,12 +797,34 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dkv1_mfma_
         const char* slot = lds + (c % R) * G::SLOT;
         // dv1 launch (registers to spare): reads two MFMAs ahead
         constexpr int kPF = kDV ? 2 : kDk1PF;
-        const floatx16 sv = OPK::template rows_x<G::RSK, kPF>(slot, qo, lane, ra.a);
-        floatx16 dp;
-        if constexpr (kDK) dp = OPV::template rows_x<G::RSV>(slot + G::VOFF, qo, lane, rbv.a);
+        floatx16 sv, dp;
+        if constexpr (F32) {
+          sv = OPK::template rows_x_hl<G::RSK>(slot, qo, lane, ra.a, ra.al);
+          if constexpr (kDK) dp = OPV::template rows_x_hl<G::RSV>(slot + G::VOFF, qo, lane, rbv.a, rbv.al);
+        } else {
+          sv = OPK::template rows_x<G::RSK, kPF>(slot, qo, lane, ra.a);
+          if constexpr (kDK) dp = OPV::template rows_x<G::RSV>(slot + G::VOFF, qo, lane, rbv.a);
+        }
         const int lo_h = klo - 4 * half, hi_h = khi - 4 * half;
         // interior chunk: every key valid for every row of the wave (uniform test)
         const bool interior = s0 <= kfirst && c >= 1 && kChunk * c <= p.wl - kChunk;
+        if constexpr (F32) {
+          // dS (MODE 1) or P (MODE 2) in fp32, then hi/lo B operands
+          float x[16];
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int kr = 8 * (e >> 2) + (e & 3);
+            const bool ok = interior || (row_ok && kr >= lo_h && kr <= hi_h);
+            const float pe = ok ? fast_exp2(fmaf(sv[e], sl2s, -(interior ? lse2r : lse2))) : 0.f;
+            if constexpr (kDK) x[e] = pe * fmaf(dp[e], dpm, dsm);
+            else x[e] = pe;
+          }
+          bf16x8 b0, b1, l0, l1;
+          OPK::pack_c_hl(x, b0, b1, l0, l1);
+          if constexpr (kDK) OPK::template tr_acc_hl<G::RSK>(acc, slot, qo, lane, b0, b1, l0, l1);
+          else OPV::template tr_acc_hl<G::RSV>(acc, slot + G::VOFF, qo, lane, b0, b1, l0, l1);
+          continue;
+        }
         // dS (MODE 1) or P (MODE 2) straight into packed bf16 pairs (B operand)
         uint32_t pk[8];
         if (interior) {  // rows outside the window: exp2(s*c - inf) = 0 with no per-key test
@@ -821,14 +858,22 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dkv1_mfma_
       float* red = (float*)lds + wid * (64 * 36);
       {
         const char* xs = kDK ? rslot + srow * G::RSK : rslot + G::VOFF + srow * G::RSV;
-        bf16x4 xv[XW / 64][2][4];
+        floatx4 xv[XW / 64][2][4];
 #pragma unroll
         for (int sl = 0; sl < XW / 64; ++sl)
 #pragma unroll
           for (int dbl = 0; dbl < 2; ++dbl)
 #pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4)
-              xv[sl][dbl][q4] = *(const bf16x4*)(xs + 2 * (64 * sl + 32 * dbl + 8 * q4 + 4 * half));
+            for (int q4 = 0; q4 < 4; ++q4) {
+              const int dd = 64 * sl + 32 * dbl + 8 * q4 + 4 * half;
+              if constexpr (F32) {
+                xv[sl][dbl][q4] = *(const floatx4*)(xs + 4 * dd);
+              } else {
+                const bf16x4 xb = *(const bf16x4*)(xs + 2 * dd);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xv[sl][dbl][q4][e] = (float)xb[e];
+              }
+            }
 #pragma unroll
         for (int sl = 0; sl < XW / 64; ++sl) {
 #pragma unroll
@@ -839,7 +884,7 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dkv1_mfma_
               const int dd = 32 * dbl + 8 * q4 + 4 * half;
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
-                const float x = row_ok ? (float)xv[sl][dbl][q4][e] : 0.f;
+                const float x = row_ok ? xv[sl][dbl][q4][e] : 0.f;
                 red[(dd + e) * 36 + n] = x * acc[db][4 * q4 + e];
               }
             }
@@ -864,30 +909,31 @@ __global__ __launch_bounds__(64 * NQ * NH, DK > 128 ? 1 : 2) void bwd_dkv1_mfma_
   for (int i = 0; i < XW / 64; ++i) sum[wid * XW + 64 * i + lane] = xrun[i];
   block_barrier();
   if (hw == 0 && jvalid) {
-    bf16* orow = kDK ? (bf16*)p.dk1 + (int64_t)j * p.dk_st + (int64_t)g * p.dk_sh
-                     : (bf16*)p.dv1 + (int64_t)j * p.dv_st + (int64_t)g * p.dv_sh;
+    const int64_t off = kDK ? (int64_t)j * p.dk_st + (int64_t)g * p.dk_sh : (int64_t)j * p.dv_st + (int64_t)g * p.dv_sh;
 #pragma unroll
     for (int i = 0; i < XW / 64; ++i) {
       float a = 0.f;
       for (int w = 0; w < NH; ++w) a += sum[(wid + w) * XW + 64 * i + lane];
-      orow[64 * i + lane] = (bf16)a;
+      if constexpr (F32) ((float*)(kDK ? p.dk1 : p.dv1))[off + 64 * i + lane] = a;
+      else ((bf16*)(kDK ? p.dk1 : p.dv1))[off + 64 * i + lane] = (bf16)a;
     }
   }
 }
 
-template <int DK, int DV, int NQ, int NH>
+template <int DK, int DV, int NQ, int NH, bool F32 = false>
 hipError_t launch_dkv1_t(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
-  constexpr int P = 1;  // two workgroups per CU (<= 80 KB of LDS each)
+  constexpr int P = 1;  // two workgroups per CU (<= 80 KB of LDS each; fp32: one)
   geo.qblocks = (p.tokens + NQ - 1) / NQ;
   geo.hsub = p.group / NH;
   geo.nblocks = geo.qblocks * p.hk;
   constexpr int NW = NQ * NH;
-  using G = TileGeom<DK, DV, kChunk + NQ - 1, NW, 32, 32>;
+  constexpr int EW = F32 ? 2 : 1;
+  using G = TileGeom<EW * DK, EW * DV, kChunk + NQ - 1, NW, 32, 32>;
   const size_t kslot = ((size_t)NW * (G::RSK + G::RSV) + 1023) / 1024 * 1024;
   const size_t ring = (size_t)(P + 1) * G::SLOT, red = (size_t)NW * 64 * 36 * sizeof(float);
   const size_t lds = (ring > red ? ring : red) + G::SLOT + kslot;
-  for (auto kern : {bwd_dkv1_mfma_kernel<DK, DV, NQ, NH, P, 1>, bwd_dkv1_mfma_kernel<DK, DV, NQ, NH, P, 2>}) {
-    if (p.dk1p && kern == bwd_dkv1_mfma_kernel<DK, DV, NQ, NH, P, 1>) continue;  // dk1 came from the dq pass
+  for (auto kern : {bwd_dkv1_mfma_kernel<DK, DV, NQ, NH, P, 1, F32>, bwd_dkv1_mfma_kernel<DK, DV, NQ, NH, P, 2, F32>}) {
+    if (p.dk1p && kern == bwd_dkv1_mfma_kernel<DK, DV, NQ, NH, P, 1, F32>) continue;  // dk1 came from the dq pass
     hipError_t e = set_lds_limit((const void*)kern, lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kern, dim3(geo.nblocks), dim3(64 * NW), lds, stream, p, geo);
@@ -897,9 +943,9 @@ hipError_t launch_dkv1_t(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
   return hipSuccess;
 }
 
-template <int DK, int DV>
+template <int DK, int DV, bool F32 = false>
 hipError_t launch_dkv1_d(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
-  return launch_dkv1_t<DK, DV, 4, 1>(p, geo, stream);
+  return launch_dkv1_t<DK, DV, 4, 1, F32>(p, geo, stream);
 }
 
 // dk1[j, g] = Σ_{head sub-groups hs of g} Σ_{query blocks qb}
@@ -1407,8 +1453,12 @@ hipError_t launch_bwd_dq_mfma(const BwdParams& p, hipStream_t stream) {
 }
 
 hipError_t launch_bwd_dkv1_mfma(const BwdParams& p, hipStream_t stream) {
-  if (!bwd_mfma_ok(p) || p.f32) return hipErrorNotSupported;
+  if (!bwd_mfma_ok(p)) return hipErrorNotSupported;
   const BwdGeo geo = base_geo(p);
+  if (p.f32) {
+    if (p.ws > 32) return hipErrorNotSupported;  // fp32: one 32-row group of short keys
+    return p.d == 64 ? launch_dkv1_d<64, 64, true>(p, geo, stream) : launch_dkv1_d<128, 128, true>(p, geo, stream);
+  }
   return by_widths<true>(p, [&](auto dk, auto dv) { return launch_dkv1_d<decltype(dk)::value, decltype(dv)::value>(p, geo, stream); });
 }
 bool bwd_dk1_fused_ok(const BwdParams& p) {

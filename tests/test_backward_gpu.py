@@ -246,8 +246,11 @@ def test_backward_bf16_separate_dk1_when_partials_do_not_fit(cuda, monkeypatch):
     monkeypatch.setattr(shim.torch, "empty", empty)
     _run(cuda, 1, 200, 4, 4, 128, 32, 96, torch.bfloat16, seed=77)
     _run(cuda, 2, 61, 6, 2, 64, 20, 70, torch.bfloat16, seed=78)
+    # fp32: the dk1 pass on the matrix cores (shape chosen so that the forward's
+    # fp32 workspace stays under the refused size)
+    _run(cuda, 1, 200, 4, 2, 128, 32, 96, torch.float32, seed=79)
     monkeypatch.undo()
-    assert len(refused) == 2, refused  # one refused partials workspace per call, then the small one
+    assert len(refused) == 3, refused  # one refused partials workspace per call, then the small one
 
 
 # ---- fp32 inputs on the matrix cores: every operand as hi + lo bf16 terms,
