@@ -272,14 +272,14 @@ def decode_cpu_leg(args, cfg, inp):
     }
 
 
-def backward_leg(args, fwd_ms, workload=None):
+def backward_leg(args, fwd_ms, workload=None, cfg=None):
     """Forward + backward (torch.autograd through the library's backward) on the
     prefill workload; nominal backward FLOPs = 2x the forward's (the reference
     counts 12*H*D*triples for forward + backward, limite_cost.py:69-73)."""
     import torch
     from archlab_amd import simplicial_attention, simplicial_varlen_attention
     from archlab_amd import workloads as W
-    cfg = {"NS": W.NS, "C2": W.C2, "C3": W.C3, "C4": W.C4}[workload or args.workload]
+    cfg = cfg or getattr(W, workload or args.workload)
     dev = torch.device("cuda:0")
     q, k1, k2, v1, v2, cu = W.prefill_inputs(cfg, device=dev)
     xs = [t.detach().requires_grad_(True) for t in (q, k1, k2, v1, v2)]
@@ -307,6 +307,7 @@ def backward_leg(args, fwd_ms, workload=None):
         "bwd_flops": flops, "bwd_tflops": flops / (bwd_ms * 1e-3) / 1e12,
         "bwd_frac_of_peak": flops / (bwd_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
         "bwd_valid_pair_flops": valid, "bwd_valid_pair_tflops": valid / (bwd_ms * 1e-3) / 1e12,
+        "dtype": str(cfg.dtype).replace("torch.", ""),
         "kernels": "bwd_dq_mfma_kernel, bwd_dkv1_mfma_kernel, bwd_dkv2_mfma_kernel (+ bwd_delta_kernel)",
     }
 
@@ -458,6 +459,16 @@ def main():
         _progress(f"decode C5: {dec['us_per_step']:.2f} us/step")
     if "fp32" in legs:
         fp32.update(fp32_prefill_leg(args))
+        # the reference's fp32 training core at its adapter geometry, forward +
+        # backward, next to the same shape in bf16
+        import dataclasses
+        f32b = backward_leg(args, None, cfg=W.DSV41)
+        b16b = backward_leg(args, None, cfg=dataclasses.replace(W.DSV41, name="DSV41-bf16", dtype=torch.bfloat16))
+        fp32["DSV41_fwd_bwd"] = _rounded(f32b)
+        fp32["DSV41_fwd_bwd"]["bf16_same_shape"] = _rounded(b16b)
+        fp32["DSV41_fwd_bwd"]["bwd_fp32_over_bf16"] = round(f32b["bwd_ms"] / b16b["bwd_ms"], 3)
+        _progress(f"fp32 DSV41 fwd+bwd: {f32b['fwd_bwd_ms']:.2f} ms (bwd {f32b['bwd_ms']:.2f} ms, "
+                  f"bf16 bwd {b16b['bwd_ms']:.2f} ms)")
         _progress("fp32: " + ", ".join(f"{k} {v.get('ms_per_step', v.get('us_per_step'))}" for k, v in fp32.items()))
     if fp32:
         out["fp32"] = fp32

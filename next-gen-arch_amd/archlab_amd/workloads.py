@@ -64,6 +64,10 @@ NS = PrefillConfig("NS-bf16-prefill-S8192", 2, 8192, 16, 16, 128, 512, 32)
 C3 = PrefillConfig("C3-bf16-varlen-gqa", 1, 32768, 32, 8, 128, 512, 32, varlen_seqs=12)
 C4 = PrefillConfig("C4-bf16-d256", 1, 16384, 8, 8, 256, 256, 64, sigma=0.5)
 C5 = PagedConfig("C5-bf16-paged-decode", 64, 32, 8, 128, 512, 32, 64, 1024, 32768)
+# The reference's DeepSeek-V4.1 adapter geometry (recipes/deepseek_v41/proposals.yaml:57-59,
+# short window 32, long window 512), whose core runs in fp32 for training
+# (deepseek_v41_adapter.py:136-144); two sequences of 8192 tokens.
+DSV41 = PrefillConfig("DSV41-fp32-adapter", 2, 8192, 8, 2, 128, 512, 32, torch.float32)
 
 
 def varlen_lengths(total: int, nseq: int, seed: int, lo: int = 256, hi: int = 6000) -> list[int]:

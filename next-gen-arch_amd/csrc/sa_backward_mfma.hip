@@ -1006,10 +1006,16 @@ __global__ __launch_bounds__(256) void bwd_dk1_sum_kernel(BwdParams p, int qbloc
 // sums to p.dkv2p and phase 2 (groups NR .. 2NR-1) starting from them and
 // writing the gradient; widths of 256 (one group per launch) always run so.
 // Without PH, phase is 0 (one launch).
-template <int DK, int DV, int MODE, int NWK, int NR, bool PH>
-__global__ __launch_bounds__(64 * NWK, DK > 128 ? 1 : 2) void bwd_dkv2_mfma_kernel(BwdParams p, int nblocks,
-                                                                                  int phase) {
+// F32: fp32 inputs (DK == DV <= 128, NR = 1): the K2 / V2 fragments from the
+// hi/lo rows (hi and lo fragments), fp32 q / dout / k1 / v1 rows in the
+// stage and the ring, A / B tile rows formed as [hi: D | lo: D] from fp32
+// products, three term pairs per product, fp32 output.
+template <int DK, int DV, int MODE, int NWK, int NR, bool PH, bool F32 = false>
+__global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_mfma_kernel(BwdParams p,
+                                                                                           int nblocks, int phase) {
+  static_assert(!F32 || (DK == DV && DK <= 128 && NR == 1 && !PH), "fp32 inputs: equal widths up to 128, one group");
   constexpr bool kDK = MODE == 1, kDV = MODE == 2;
+  constexpr int EW = F32 ? 2 : 1;  // bf16 units per element of an LDS row
   constexpr int kKvRing = 64 * NR;  // k1 / v1 ring rows (a power of two)
   constexpr int KB = 32 * NWK;    // keys per workgroup
   constexpr int RPW = 32 / NWK;   // A / B rows formed per wave and step
@@ -1021,9 +1027,9 @@ __global__ __launch_bounds__(64 * NWK, DK > 128 ? 1 : 2) void bwd_dkv2_mfma_kern
   using OPK = BwdOps<DK>;
   using OPV = BwdOps<DV>;
   // A / B tile row strides (padded: row and transposing reads)
-  constexpr int RSA = 2 * DK + 32, RSB = 2 * DV + 32;
+  constexpr int RSA = 2 * EW * DK + 32, RSB = 2 * EW * DV + 32;
   constexpr int TA = 32 * RSA, TAB = TA + 32 * RSB;  // one A tile, one A + B pair
-  constexpr int RBK = 2 * DK, RBV = 2 * DV;  // k1 / v1 row bytes
+  constexpr int RBK = 2 * EW * DK, RBV = 2 * EW * DV;  // k1 / v1 row bytes (q / dout rows alike)
   constexpr int RKV = RBK + RBV;             // ring row: k1 then v1
   constexpr int SS = (2 * RKV + 1023) / 1024 * 1024, SI = SS / 1024;  // stage slot bytes, DMA instructions
   extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -1052,14 +1058,22 @@ __global__ __launch_bounds__(64 * NWK, DK > 128 ? 1 : 2) void bwd_dkv2_mfma_kern
 
   // K2 / V2 rows of the wave's keys as B operands (k = d): lane (n, half)
   // holds d = 16t + 8*half .. +7 of key kw.
-  const bf16* k2r = (const bf16*)p.k2 + (int64_t)kwc * p.k_st + kvg_k;
-  const bf16* v2r = (const bf16*)p.v2 + (int64_t)kwc * p.v_st + kvg_v;
+  // (fp32: the hi/lo rows [tokens][hk][2 D], hi fragments in kf / vf, lo in kfl / vfl)
+  const bf16* k2r = F32 ? p.k2s + ((int64_t)kwc * p.hk + g) * 2 * DK : (const bf16*)p.k2 + (int64_t)kwc * p.k_st + kvg_k;
+  const bf16* v2r = F32 ? p.v2s + ((int64_t)kwc * p.hk + g) * 2 * DV : (const bf16*)p.v2 + (int64_t)kwc * p.v_st + kvg_v;
   bf16x8 kf[DK / 16], vf[kDK ? DV / 16 : 1];
+  bf16x8 kfl[F32 ? DK / 16 : 1], vfl[F32 && kDK ? DV / 16 : 1];
 #pragma unroll
-  for (int t = 0; t < DK / 16; ++t) kf[t] = *(const bf16x8*)(k2r + 16 * t + 8 * half);
+  for (int t = 0; t < DK / 16; ++t) {
+    kf[t] = *(const bf16x8*)(k2r + 16 * t + 8 * half);
+    if constexpr (F32) kfl[t] = *(const bf16x8*)(k2r + DK + 16 * t + 8 * half);
+  }
   if constexpr (kDK) {
 #pragma unroll
-    for (int t = 0; t < DV / 16; ++t) vf[t] = *(const bf16x8*)(v2r + 16 * t + 8 * half);
+    for (int t = 0; t < DV / 16; ++t) {
+      vf[t] = *(const bf16x8*)(v2r + 16 * t + 8 * half);
+      if constexpr (F32) vfl[t] = *(const bf16x8*)(v2r + DV + 16 * t + 8 * half);
+    }
   }
   floatx16 acc[XW / 32];  // dK2^T or dV2^T
 #pragma unroll
@@ -1108,10 +1122,12 @@ __global__ __launch_bounds__(64 * NWK, DK > 128 ? 1 : 2) void bwd_dkv2_mfma_kern
       int b = 1024 * k + 16 * fresh_lane();
       if (b >= 2 * RKV) b = 0;
       const bf16* src;
-      if (b < RBK) src = (const bf16*)p.q + (int64_t)t * p.q_st + (int64_t)h * p.q_sh + b / 2;
-      else if (b < RKV) src = (const bf16*)p.dout + (int64_t)t * p.do_st + (int64_t)h * p.do_sh + (b - RBK) / 2;
-      else if (b < RKV + RBK) src = (const bf16*)p.k1 + (int64_t)t * p.k_st + kvg_k + (b - RKV) / 2;
-      else src = (const bf16*)p.v1 + (int64_t)t * p.v_st + kvg_v + (b - RKV - RBK) / 2;
+      // (element offsets scaled by EW: fp32 rows viewed as bf16 units)
+      if (b < RBK) src = (const bf16*)p.q + EW * ((int64_t)t * p.q_st + (int64_t)h * p.q_sh) + b / 2;
+      else if (b < RKV)
+        src = (const bf16*)p.dout + EW * ((int64_t)t * p.do_st + (int64_t)h * p.do_sh) + (b - RBK) / 2;
+      else if (b < RKV + RBK) src = (const bf16*)p.k1 + EW * ((int64_t)t * p.k_st + kvg_k) + (b - RKV) / 2;
+      else src = (const bf16*)p.v1 + EW * ((int64_t)t * p.v_st + kvg_v) + (b - RKV - RBK) / 2;
       dma16(src, stage + x.slot * SS + 1024 * k);
     }
   };
@@ -1133,8 +1149,8 @@ __global__ __launch_bounds__(64 * NWK, DK > 128 ? 1 : 2) void bwd_dkv2_mfma_kern
     const int jj = idx / (RKV / 16), w = idx % (RKV / 16);  // w: 16-byte segment of the ring row
     const int j = tfirst - (32 * (NR + r0) - 1) + jj;
     if (j >= 0) {
-      const bf16* src = w < RBK / 16 ? (const bf16*)p.k1 + (int64_t)j * p.k_st + kvg_k + 8 * w
-                                     : (const bf16*)p.v1 + (int64_t)j * p.v_st + kvg_v + 8 * (w - RBK / 16);
+      const bf16* src = w < RBK / 16 ? (const bf16*)p.k1 + EW * ((int64_t)j * p.k_st + kvg_k) + 8 * w
+                                     : (const bf16*)p.v1 + EW * ((int64_t)j * p.v_st + kvg_v) + 8 * (w - RBK / 16);
       *(uint4*)(ring + (j % kKvRing) * RKV + 16 * w) = *(const uint4*)src;
     }
   }
@@ -1147,7 +1163,41 @@ __global__ __launch_bounds__(64 * NWK, DK > 128 ? 1 : 2) void bwd_dkv2_mfma_kern
   auto form = [&](Step x, int b) {
     const int t = x.t;
     const char* sg_row = stage + x.slot * SS;
-    if constexpr (DK == DV) {  // A and B rows side by side: one row and segment per lane
+    if constexpr (F32) {
+      // fp32 rows: one row and 4 elements (16 source bytes) per lane; the
+      // products q ⊙ k1 and dout ⊙ v1 split into hi (row elements 4 sg ..)
+      // and lo (elements D + 4 sg ..) bf16 terms
+      constexpr int SEGS = DK / 4;
+      static_assert(RPW * SEGS % 64 == 0, "whole lanes per formed row block");
+#pragma unroll
+      for (int u = 0; u < RPW * SEGS / 64; ++u) {
+        char* At = tiles + b * TAB;
+        char* Bt = At + TA;
+        const int idx = u * 64 + lane;
+        const int i = RPW * wid + idx / SEGS, sg = idx % SEGS;  // tile row, 4-element group
+        const int j = max(t - 31 + i, 0);
+        const char* kvrow = j == t ? sg_row + RKV : ring + (j % kKvRing) * RKV;
+        const floatx4 qv = *(const floatx4*)(sg_row + 16 * sg);
+        const floatx4 gv = *(const floatx4*)(sg_row + RBK + 16 * sg);
+        const floatx4 kv = *(const floatx4*)(kvrow + 16 * sg);
+        const floatx4 vv = *(const floatx4*)(kvrow + RBK + 16 * sg);
+        bf16x4 ah, al, bh, bl;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          bf16 h_, l_;
+          split_bf16(qv[e] * kv[e], h_, l_);
+          ah[e] = h_;
+          al[e] = l_;
+          split_bf16(gv[e] * vv[e], h_, l_);
+          bh[e] = h_;
+          bl[e] = l_;
+        }
+        *(bf16x4*)(At + i * RSA + 8 * sg) = ah;
+        *(bf16x4*)(At + i * RSA + 2 * DK + 8 * sg) = al;
+        *(bf16x4*)(Bt + i * RSB + 8 * sg) = bh;
+        *(bf16x4*)(Bt + i * RSB + 2 * DV + 8 * sg) = bl;
+      }
+    } else if constexpr (DK == DV) {  // A and B rows side by side: one row and segment per lane
       constexpr int SEGS = DK / 8;  // 16-byte segments per row
       static_assert(RPW * SEGS % 64 == 0, "whole lanes per formed row block");
 #pragma unroll
@@ -1288,8 +1338,13 @@ __global__ __launch_bounds__(64 * NWK, DK > 128 ? 1 : 2) void bwd_dkv2_mfma_kern
     const char* Bt = At + TA;
     floatx16 sv, dp;
     if (!skip) {
-      sv = OPK::template rows_x<RSA, kPF>(At, 0, lane, kf);  // C[j][key]
-      if constexpr (kDK) dp = OPV::template rows_x<RSB, kPF>(Bt, 0, lane, vf);
+      if constexpr (F32) {
+        sv = OPK::template rows_x_hl<RSA>(At, 0, lane, kf, kfl);  // C[j][key]
+        if constexpr (kDK) dp = OPV::template rows_x_hl<RSB>(Bt, 0, lane, vf, vfl);
+      } else {
+        sv = OPK::template rows_x<RSA, kPF>(At, 0, lane, kf);  // C[j][key]
+        if constexpr (kDK) dp = OPV::template rows_x<RSB, kPF>(Bt, 0, lane, vf);
+      }
     }
     // the next step's rows are formed after this step's S (and dP) MFMAs are
     // issued: the VALU work runs while the matrix cores work (the two waves
@@ -1303,6 +1358,23 @@ __global__ __launch_bounds__(64 * NWK, DK > 128 ? 1 : 2) void bwd_dkv2_mfma_kern
     // group r: the probabilities (dS or P) from its scores, then
     // dK2^T += A_t^T · dS^T, or dV2^T += B_t^T · P^T
     auto accumulate = [&](const floatx16& s_, const floatx16& dp_, int ilo_r, const char* At_r, const char* Bt_r) {
+      if constexpr (F32) {
+        // dS (dK2 launch) or P (dV2 launch) in fp32, as hi/lo B operands
+        float x[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int ie = 8 * (e >> 2) + 4 * half + (e & 3);
+          const bool ok = kok && ie >= ilo_r;
+          const float pe = ok ? fast_exp2(fmaf(s_[e], sl2s, -lse2)) : 0.f;
+          if constexpr (kDK) x[e] = pe * fmaf(dp_[e], dpm, dsm);
+          else x[e] = pe;
+        }
+        bf16x8 b0, b1, l0, l1;
+        OPK::pack_c_hl(x, b0, b1, l0, l1);
+        if constexpr (kDK) OPK::template tr_acc_hl<RSA>(acc, At_r, 0, lane, b0, b1, l0, l1);
+        else OPV::template tr_acc_hl<RSB>(acc, Bt_r, 0, lane, b0, b1, l0, l1);
+        return;
+      }
       uint32_t pk[8];  // bf16(dS) (dK2 launch) or bf16(P) (dV2 launch)
       if (ilo_r <= 0) {  // every row valid (uniform test); keys outside: exp2(s*c - inf) = 0
         const float lse2k = kok ? lse2 : INFINITY;
@@ -1353,6 +1425,18 @@ __global__ __launch_bounds__(64 * NWK, DK > 128 ? 1 : 2) void bwd_dkv2_mfma_kern
         for (int e = 0; e < 4; ++e) x[e] = acc[db][4 * q4 + e];
         *(floatx4*)(part + 32 * db + 8 * q4 + 4 * half) = x;
       }
+  } else if (F32 && kvalid) {
+    float* orow = kDK ? (float*)p.dk2 + (int64_t)kw * p.dk_st + (int64_t)g * p.dk_sh
+                      : (float*)p.dv2 + (int64_t)kw * p.dv_st + (int64_t)g * p.dv_sh;
+#pragma unroll
+    for (int db = 0; db < XW / 32; ++db)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        floatx4 a;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a[e] = acc[db][4 * q4 + e];
+        *(floatx4*)(orow + 32 * db + 8 * q4 + 4 * half) = a;
+      }
   } else if (kvalid) {
     bf16* orow = kDK ? (bf16*)p.dk2 + (int64_t)kw * p.dk_st + (int64_t)g * p.dk_sh
                      : (bf16*)p.dv2 + (int64_t)kw * p.dv_st + (int64_t)g * p.dv_sh;
@@ -1369,19 +1453,21 @@ __global__ __launch_bounds__(64 * NWK, DK > 128 ? 1 : 2) void bwd_dkv2_mfma_kern
   }
 }
 
-template <int DK, int DV, int NR, bool PH>
+template <int DK, int DV, int NR, bool PH, bool F32 = false>
 hipError_t launch_dkv2_t(const BwdParams& p, hipStream_t stream) {
-  constexpr int RSA = 2 * DK + 32, RSB = 2 * DV + 32, RKV = 2 * (DK + DV);
+  constexpr int EW = F32 ? 2 : 1;
+  constexpr int RSA = 2 * EW * DK + 32, RSB = 2 * EW * DV + 32, RKV = 2 * EW * (DK + DV);
   constexpr int SS = (2 * RKV + 1023) / 1024 * 1024;  // stage slot
   // one 8-wave workgroup per CU when both widths are 128, 4-wave workgroups
   // otherwise (a wave forms 32 / NWK rows per step in whole 64-lane
-  // instructions; at DK = 256 the 4 waves hold one workgroup per CU)
-  constexpr int NWK = DK == 128 && DV == 128 ? 8 : 4;
+  // instructions; at DK = 256 the 4 waves hold one workgroup per CU; fp32
+  // inputs: 4 waves, one per SIMD, for the hi/lo fragments)
+  constexpr int NWK = DK == 128 && DV == 128 && !F32 ? 8 : 4;
   const size_t lds = (size_t)2 * NR * 32 * (RSA + RSB) + (size_t)64 * NR * RKV + 3 * SS + (size_t)NWK * 64 * 16;
   const int nblocks = (p.tokens + 32 * NWK - 1) / (32 * NWK) * p.hk;
   // more short-key rows than one launch's LDS holds: two launches (phases 1, 2)
   const bool two = PH && p.ws > 32 * NR;
-  for (auto kern : {bwd_dkv2_mfma_kernel<DK, DV, 1, NWK, NR, PH>, bwd_dkv2_mfma_kernel<DK, DV, 2, NWK, NR, PH>}) {
+  for (auto kern : {bwd_dkv2_mfma_kernel<DK, DV, 1, NWK, NR, PH, F32>, bwd_dkv2_mfma_kernel<DK, DV, 2, NWK, NR, PH, F32>}) {
     hipError_t e = set_lds_limit((const void*)kern, lds);
     if (e != hipSuccess) return e;
     for (int phase = two ? 1 : 0; phase <= (two ? 2 : 0); ++phase) {
@@ -1477,9 +1563,13 @@ hipError_t launch_bwd_dk1_sum(const BwdParams& p, hipStream_t stream) {
 }
 
 hipError_t launch_bwd_dkv2_mfma(const BwdParams& p, hipStream_t stream) {
+  if (p.f32) {  // fp32: one 32-row group of short keys
+    if (!bwd_mfma_ok(p) || p.ws > 32) return hipErrorNotSupported;
+    return p.d == 64 ? launch_dkv2_t<64, 64, 1, false, true>(p, stream) : launch_dkv2_t<128, 128, 1, false, true>(p, stream);
+  }
   // one launch covers 64 short keys (32 at DK = 256); two launches over the fp32 partial twice that
   const int one = p.d > 128 ? 32 : 64;
-  if (!bwd_mfma_ok(p) || p.f32 || p.ws > 2 * one || (p.ws > one && !p.dkv2p)) return hipErrorNotSupported;
+  if (!bwd_mfma_ok(p) || p.ws > 2 * one || (p.ws > one && !p.dkv2p)) return hipErrorNotSupported;
   return by_widths<true>(p, [&](auto dk, auto dv) { return launch_dkv2_d<decltype(dk)::value, decltype(dv)::value>(p, stream); });
 }
 

@@ -334,7 +334,7 @@ def test_paged_accepts_the_reference_mixed_index_dtypes_before_launch():
 @pytest.mark.parametrize("dtype,hq,hk,d,dv,ws,fused", [
     ("bf16", 4, 4, 128, 128, 32, True), ("bf16", 6, 2, 64, 64, 20, True), ("bf16", 8, 2, 128, 128, 32, True),
     ("bf16", 4, 2, 64, 64, 32, True), ("bf16", 4, 4, 128, 64, 32, True), ("bf16", 6, 2, 64, 128, 8, True),
-    ("bf16", 4, 4, 128, 128, 40, False), ("f32", 4, 4, 64, 64, 32, False), ("bf16", 4, 4, 256, 128, 32, True),
+    ("bf16", 4, 4, 128, 128, 40, False), ("f32", 4, 4, 64, 64, 32, True), ("f32", 6, 2, 128, 128, 20, True), ("bf16", 4, 4, 256, 128, 32, True),
     ("bf16", 8, 2, 256, 256, 16, True), ("bf16", 4, 4, 256, 64, 32, False), ("bf16", 4, 4, 256, 256, 40, False),
     ("bf16", 4, 2, 256, 128, 64, False), ("bf16", 4, 4, 256, 256, 65, False), ("bf16", 4, 2, 128, 64, 100, False),
     ("bf16", 4, 4, 64, 64, 128, False), ("bf16", 4, 4, 64, 64, 129, False), ("f32", 4, 4, 128, 128, 100, False)])
@@ -342,7 +342,7 @@ def test_backward_workspace_reserves_dk1_partials_for_fused_shapes(dtype, hq, hk
     """The backward workspace holds delta and dlse rows ([tokens, hq] fp32 each,
     256-byte rounded) and, where dk1 comes from the dq pass (bf16, score width
     D and value width each 64 or 128, or D = 256 over values of 128 or 256;
-    short window <= 32), the partials:
+    short window <= 32; fp32 with equal widths of 64 or 128 as well), the partials:
     31 + NQ fp32 rows of D per
     dq workgroup of NQ queries x 4 / NQ heads (NQ = 4, 2, 1 for GQA groups
     that are odd, even, multiples of 4)."""
@@ -368,15 +368,21 @@ def test_backward_workspace_reserves_dk1_partials_for_fused_shapes(dtype, hq, hk
     widths = (d in (64, 128) and dv in (64, 128)) or (d == 256 and dv in (128, 256))
     phased = dtype == "bf16" and widths and one < ws <= 2 * one
     dkv2 = (tokens * hk * (d + dv) * 4 + 255) // 256 * 256 if phased else 0
-    assert lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args)) == 2 * rows + part + dkv2
+    # fp32 on the matrix cores (equal widths of 64 or 128, short window <= 32):
+    # k2 and v2 as hi/lo bf16 rows, [tokens][hk][2 d] each
+    f32_mfma = dtype == "f32" and d == dv and d in (64, 128) and ws <= 32
+    split = 2 * ((tokens * hk * d * 4 + 255) // 256 * 256) if f32_mfma else 0
+    assert lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args)) == 2 * rows + part + dkv2 + split
     if fused:
         # past 8 GiB of partials the separate dk1 pass runs: no partials reserved
         big = int((8 << 30) / per_query) // 4 * 4 + 8
         args.fwd.total_tokens = args.fwd.seqlen = big
         rows = (big * hq * 4 + 255) // 256 * 256
-        assert lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args)) == 2 * rows
+        split = 2 * ((big * hk * d * 4 + 255) // 256 * 256) if f32_mfma else 0
+        assert lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args)) == 2 * rows + split
     # a caller short of memory selects the separate dk1 pass: no partials reserved
     args.fwd.total_tokens = args.fwd.seqlen = tokens
     args.fwd.flags = _native.SA_FLAG_SEPARATE_DK1
     rows = (tokens * hq * 4 + 255) // 256 * 256
-    assert lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args)) == 2 * rows + dkv2
+    split = 2 * ((tokens * hk * d * 4 + 255) // 256 * 256) if f32_mfma else 0
+    assert lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args)) == 2 * rows + dkv2 + split
