@@ -50,12 +50,13 @@ def _args():
     ap.add_argument("--decode-steps", type=int, default=200)
     ap.add_argument("--bwd-steps", type=int, default=10)
     ap.add_argument("--bwd-configs", default="C3,C4", help="further workloads of the backward leg")
-    ap.add_argument("--legs", default="prefill,configs,decode,fp32,backward,cpu")
+    ap.add_argument("--legs", default="prefill,configs,decode,global,fp32,backward,cpu")
     ap.add_argument("--configs", default="C2,C3,C4", help="prefill configurations of the configs leg")
     ap.add_argument("--workload", default="NS", help="prefill workload: NS, C2, C3, C4")
     ap.add_argument("--cpu-positions", type=int, default=256)
     ap.add_argument("--cpu-decode-tokens", type=int, default=64)
     ap.add_argument("--fp32-steps", type=int, default=5)
+    ap.add_argument("--global-steps", type=int, default=20)
     return ap.parse_args()
 
 
@@ -223,6 +224,8 @@ def decode_leg(args):
         "l2_flushed": True, "flush": "1 GiB read between steps",
         "us_per_step_after_write_flush": wmed_ms * 1e3,
     }
+    if "global" in set(args.legs.split(",")):
+        res["global_layer"] = global_layer_leg(args, cfg, inp, flush)
     traffic = measured_traffic("paged_mfma_kernel", "C5")
     res["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                        "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic}
@@ -231,6 +234,38 @@ def decode_leg(args):
     del inp, flush_buf
     torch.cuda.empty_cache()
     return res, fp32_q
+
+
+def global_layer_leg(args, cfg, inp, flush):
+    """The reference's serving call on a global layer (serving.py:49, :80-83):
+    fp32 query, long_window = 1 << 30 (every key of the context), bf16 caches
+    at the C5 contexts and block table; GQA group 4 (C5's 32 / 8 heads) and
+    group 1 (8 / 8 heads over the same caches)."""
+    import dataclasses
+    import torch
+    from archlab_amd import simplicial_paged_attention
+    from archlab_amd import workloads as W
+    from archlab_amd.architectures.simplicial_paged import paged_plan
+    out = {}
+    capacity = inp["block_table"].shape[1] * cfg.page
+    for name, hq in (("G4_fp32_q", cfg.heads_q), ("G1_fp32_q", cfg.heads_kv)):
+        q = inp["q"][:, :hq].float().contiguous()
+        a = (q, inp["short_cache"], inp["long_cache"], inp["block_table"], inp["token_seq"], inp["token_pos"])
+        kw = dict(short_window=cfg.w2, long_window=1 << 30, scale=1.0)
+        kname, splits, ws = paged_plan(*a, **kw)
+        mean_ms, med_ms, _ = _time_kernel(lambda: simplicial_paged_attention(*a, return_lse=True, **kw),
+                                          args.global_steps, 3, flush=flush)
+        g = dataclasses.replace(cfg, heads_q=hq, w1=capacity)
+        nbytes = W.paged_bytes(g, inp["ctx"], out_bytes=4) + q.numel() * 2  # fp32 q: 4 bytes, not 2
+        out[name] = {"workload": f"{cfg.name} global layer: HQ {hq} / HKV {cfg.heads_kv}, fp32 query, "
+                                 f"long_window 2^30 (contexts {int(inp['ctx'].min())}-{int(inp['ctx'].max())})",
+                     "us_per_step": round(med_ms * 1e3, 2), "tok_per_s": round(cfg.batch / (med_ms * 1e-3), 1),
+                     "algorithmic_bytes_per_step": nbytes,
+                     "achieved_gbs": round(nbytes / (med_ms * 1e-3) / 1e9, 1),
+                     "hbm_frac": round(nbytes / (med_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                     "kernel": kname, "splits": splits, "workspace_bytes": ws}
+        _progress(f"global layer {name}: {med_ms * 1e3:.1f} us/step, splits {splits}")
+    return out
 
 
 def decode_cpu_leg(args, cfg, inp):

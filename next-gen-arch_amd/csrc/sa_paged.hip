@@ -65,8 +65,11 @@ constexpr int kSegChunks = kPosCache / kChunk;  // chunks of one such segment
 // QF32: fp32 query over bf16 caches (the reference's serving input,
 // serving.py:83): a = q ⊙ k1 and P stay fp32-accurate through hi/lo bf16
 // terms (RowBlock HL), twice the MFMA work of the bf16 kernel.
+// Workgroups of one or two waves hold one wave per SIMD whatever their
+// register count (two workgroups per CU), so they may use the whole register
+// file; four-wave workgroups are bounded to two waves per SIMD.
 template <int D, int NW, int P, bool MULTI, bool QF32>
-__global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel(PagedParams p) {
+__global__ __launch_bounds__(64 * NW, (D >= 256 || NW < 4 ? 1 : 2)) void paged_mfma_kernel(PagedParams p) {
   using G = FwdGeom<D, D, kChunk, NW>;
   using RB = RowBlock<D, D, QF32>;
   constexpr bool kPipelined = D <= 128 && P >= 2;  // second score tile fits the registers up to D = 128
@@ -177,10 +180,23 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
     if (with_short && stage && wid == 0 && lane < 32) soffs[lane] = soff;  // row n of the short slot
   };
 
-  // this lane's tile row / segment / tensor for each of its DMA instructions
-  int drow[NI], dseg[NI], dv[NI];
+  // this lane's tile row / segment / tensor for each of its DMA instructions:
+  // kept in registers, or, with many instructions per wave (one-wave
+  // workgroups at widths of 256: 3 x 34 values), decoded again at each use
+  // from a fresh lane id
+  constexpr bool kKeepSlots = NI <= 20;
+  int drow[kKeepSlots ? NI : 1], dseg[kKeepSlots ? NI : 1], dv[kKeepSlots ? NI : 1];
+  if constexpr (kKeepSlots) {
 #pragma unroll
-  for (int k = 0; k < NI; ++k) G::decode(wid, k, lane, dv[k], drow[k], dseg[k]);
+    for (int k = 0; k < NI; ++k) G::decode(wid, k, lane, dv[k], drow[k], dseg[k]);
+  }
+  auto slot_of = [&](int k, int& v_, int& row_, int& seg_) {
+    if constexpr (kKeepSlots) {
+      v_ = dv[k], row_ = drow[k], seg_ = dseg[k];
+    } else {
+      G::decode(wid, k, fresh_lane(), v_, row_, seg_);
+    }
+  };
 
   // tile rows outside [lo2, pos] re-read the nearest valid row (masked later);
   // every row offset is read from LDS before the first DMA is issued
@@ -191,13 +207,17 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
     static_for<0, (NI + KG - 1) / KG>([&](auto kg) {
       constexpr int kb = decltype(kg)::value * KG;
       int64_t off[KG];
+      int tv[KG], tseg[KG];
 #pragma unroll
       for (int k = 0; k < KG; ++k)
-        if (kb + k < NI) off[k] = roff[min(min(max(k0 + drow[kb + k], lo2), pos) - seg_lo, kPosCache - 1)];
+        if (kb + k < NI) {
+          int trow;
+          slot_of(kb + k, tv[k], trow, tseg[k]);
+          off[k] = roff[min(min(max(k0 + trow, lo2), pos) - seg_lo, kPosCache - 1)];
+        }
 #pragma unroll
       for (int k = 0; k < KG; ++k)
-        if (kb + k < NI)
-          dma16(p.lc + off[k] + (dv[kb + k] ? p.lc_a : 0) + dseg[kb + k] * 8, G::dst(slot, wid, kb + k));
+        if (kb + k < NI) dma16(p.lc + off[k] + (tv[k] ? p.lc_a : 0) + tseg[k] * 8, G::dst(slot, wid, kb + k));
     });
   };
 
@@ -219,8 +239,11 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 ? 1 : 2)) void paged_mfma_kernel
       if (first && stage) {
         // the short rows: NI DMA instructions per wave, ring-slot geometry
 #pragma unroll
-        for (int k = 0; k < NI; ++k)
-          dma16(p.sc + soffs[drow[k]] + (dv[k] ? p.sc_a : 0) + dseg[k] * 8, G::dst(sslot, wid, k));
+        for (int k = 0; k < NI; ++k) {
+          int sv_, srow_, sseg_;
+          slot_of(k, sv_, srow_, sseg_);
+          dma16(p.sc + soffs[srow_] + (sv_ ? p.sc_a : 0) + sseg_ * 8, G::dst(sslot, wid, k));
+        }
         // the q rows of the workgroup's tasks (wave 0): lane -> row, 16-byte segment
         if (wid == 0) {
           constexpr int kQI = (NW * QB + 1023) / 1024;
