@@ -197,6 +197,27 @@ def _prefill_autograd(q, k1, k2, v1, v2, short_window, long_window, scale, cu_se
                     return_lse, kernel)
 
 
+def _padded_width(d, dv, dtype, kernel):
+    """Width to which a call with score width ``d`` and value width ``dv``
+    is zero-padded to run on the matrix cores, or None.  Widths 16 and 32
+    (the reference's qualification gate runs D = 32,
+    qualification/simplicial_attention.py:42-44; its scratch-scaling recipes
+    use D = 16) pad to 64 (or to the other width): zero coordinates add
+    exactly nothing to a score, padded value columns are sliced off, and the
+    backward reaches the unpadded tensors through the pad.  Only for
+    ``kernel="auto"``; "mfma" and "generic" take the shapes as given."""
+    if kernel != "auto" or (d >= 64 and dv >= 64):
+        return None
+    w = max(64, d, dv)
+    if w not in (64, 128, 256) or (dtype == torch.float32 and w > 128):
+        return None
+    return w
+
+
+def _pad_last(x, w):
+    return x if x.shape[-1] == w else torch.nn.functional.pad(x, (0, w - x.shape[-1]))
+
+
 def simplicial_attention(q, k1, k2, v1, v2, short_window, long_window, *, scale=None,
                          return_lse=False, kernel="auto"):
     """Drop-in for ``simplicial_attention`` (simplicial_attention.py:77-97), forward only.
@@ -206,8 +227,9 @@ def simplicial_attention(q, k1, k2, v1, v2, short_window, long_window, *, scale=
     natural-log LSE [B,N,HQ] in float32.  ``kernel`` selects the
     implementation: "auto" (bf16 with D == DV in {64,128,256}, or with
     (D, DV) = (128, 64) / (256, 128) as the determinant expansion produces,
-    runs on the MFMA kernel, everything else on the portable kernel), "mfma"
-    (raise if not covered) or "generic".
+    and fp32 with D == DV in {64, 128} run on the MFMA kernel; widths 16 and
+    32 are zero-padded to 64 to run there too; everything else on the
+    portable kernel), "mfma" (raise if not covered) or "generic".
 
     Inputs that require grad get gradients from the library's backward
     (``sa_prefill_bwd``: atomics-free, bitwise reproducible; MFMA tiles for
@@ -222,11 +244,15 @@ def simplicial_attention(q, k1, k2, v1, v2, short_window, long_window, *, scale=
     _kernel_checks(q, v1.shape[-1], q.shape[-1])
     b, n, hq, d = q.shape
     hk, dv = k1.shape[2], v1.shape[-1]
-    q_, k1_, k2_ = (x.contiguous().view(b * n, -1, d) for x in (q, k1, k2))
-    v1_, v2_ = (x.contiguous().view(b * n, hk, dv) for x in (v1, v2))
+    w = _padded_width(d, dv, q.dtype, kernel)
+    if w is not None:
+        q, k1, k2, v1, v2 = (_pad_last(x, w) for x in (q, k1, k2, v1, v2))
+    dp, dvp = q.shape[-1], v1.shape[-1]
+    q_, k1_, k2_ = (x.contiguous().view(b * n, -1, dp) for x in (q, k1, k2))
+    v1_, v2_ = (x.contiguous().view(b * n, hk, dvp) for x in (v1, v2))
     out, lse = _prefill_autograd(q_, k1_, k2_, v1_, v2_, short_window, long_window, scale, None, b, n,
                                  return_lse, kernel)
-    out = out.view(b, n, hq, dv)
+    out = out.view(b, n, hq, dvp)[..., :dv]
     if return_lse:
         return out, lse.view(b, n, hq)
     return out
@@ -254,23 +280,32 @@ def simplicial_varlen_attention(q, k1, k2, v1, v2, cu_seqlens, short_window, lon
             or cu_seqlens.device != q.device):
         raise ValueError("cu_seqlens must be int32 [num_seqs + 1] on the input device")
     t, hq, d = q.shape
+    dv = v1.shape[-1]
+    w = _padded_width(d, dv, q.dtype, kernel)
+    if w is not None:
+        q, k1, k2, v1, v2 = (_pad_last(x, w) for x in (q, k1, k2, v1, v2))
     q_, k1_, k2_, v1_, v2_ = (x.contiguous() for x in (q, k1, k2, v1, v2))
     out, lse = _prefill_autograd(q_, k1_, k2_, v1_, v2_, short_window, long_window, scale,
                                  cu_seqlens.contiguous(), cu_seqlens.numel() - 1, 0, return_lse, kernel)
+    out = out[..., :dv]
     return (out, lse) if return_lse else out
 
 
 def prefill_kernel_name(q, k1, v1, *, kernel="auto"):
-    """Which kernel family ('mfma' or 'generic') a dense call with these shapes runs."""
+    """Which kernel family ('mfma' or 'generic') a dense call with these shapes
+    runs ('mfma' also for widths the shim zero-pads onto the matrix cores)."""
     lib = _native.load()
     b, n, hq, d = q.shape
+    hk, dv = k1.shape[2], v1.shape[-1]
+    w = _padded_width(d, dv, q.dtype, kernel)
+    if w is not None:
+        d = dv = w
     args = _native.PrefillArgs(
         q=16, k1=16, k2=16, v1=16, v2=16, out=16,
-        q_stride_t=hq * d, q_stride_h=d, k_stride_t=k1.shape[2] * d, k_stride_h=d,
-        v_stride_t=k1.shape[2] * v1.shape[-1], v_stride_h=v1.shape[-1],
-        o_stride_t=hq * v1.shape[-1], o_stride_h=v1.shape[-1], lse_stride_t=hq,
-        num_seqs=b, seqlen=n, total_tokens=b * n, heads_q=hq, heads_kv=k1.shape[2], head_dim=d,
-        value_dim=v1.shape[-1], short_window=1, long_window=1, scale=1.0,
+        q_stride_t=hq * d, q_stride_h=d, k_stride_t=hk * d, k_stride_h=d,
+        v_stride_t=hk * dv, v_stride_h=dv, o_stride_t=hq * dv, o_stride_h=dv, lse_stride_t=hq,
+        num_seqs=b, seqlen=n, total_tokens=b * n, heads_q=hq, heads_kv=hk, head_dim=d,
+        value_dim=dv, short_window=1, long_window=1, scale=1.0,
         dtype=_native.dtype_code(q.dtype), flags=_kernel_flag(kernel))
     # a call passes the workspace the fp32 matrix-core path asks for
     args.workspace_bytes = lib.sa_prefill_workspace_bytes(ctypes.byref(args))

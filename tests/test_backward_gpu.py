@@ -292,6 +292,14 @@ def test_backward_fp32_matrix_cores_varlen_lse_and_repeatable(cuda):
     assert not all(torch.equal(a, b) for a, b in zip(runs["auto"][0], runs["generic"][0]))
 
 
+@pytest.mark.parametrize("d,dv", [(16, 16), (32, 32), (32, 64)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_backward_narrow_widths_padded_onto_matrix_cores(cuda, d, dv, dtype):
+    """Widths 16 and 32 zero-padded onto the matrix-core passes: the gradients
+    of the unpadded tensors come back through the pad."""
+    _run(cuda, 1, 90, 4, 2, d, 16, 48, dtype, dv=dv, seed=d + dv)
+
+
 # ---- dk2 / dv2 on the matrix cores with short windows of 33-64 (two 32-row
 # groups of short keys per step) ----------------------------------------------------
 

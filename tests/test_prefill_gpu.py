@@ -415,6 +415,43 @@ def test_contract_errors(cuda):
         attn(*(t.float()[..., :32] for t in x), 2, 4, kernel="mfma")  # fp32 at D = 32
 
 
+@pytest.mark.parametrize("d,dv", [(16, 16), (32, 32), (32, 64), (16, 128)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_narrow_widths_padded_onto_matrix_cores(cuda, d, dv, dtype):
+    """Widths 16 and 32 run on the matrix cores zero-padded to 64 (or to the
+    other width).  fp32: the oracle at 1e-4.  bf16: the oracle with the
+    reference kernel's rounding point of a = bf16(q ⊙ k1) (simplicial_kernels.py:35)
+    at LSE 1e-4 and out 4e-3 (+ one bf16 ulp), and the plain fp32 oracle at
+    out 4e-2 / LSE 4e-3: with 16 or 32 terms per score that rounding moves
+    the result further than at the BASELINE widths (64-256), the same for the
+    reference kernel."""
+    attn, varlen, name = _api()
+    x = rand_inputs(1, 2, 4, 2, d, dv=dv, dtype=dtype)
+    assert name(x[0], x[1], x[3]) == "mfma"
+    if dtype == torch.float32:
+        _check(cuda, 2, 120, 4, 2, d, 16, 48, dtype, seed=d + dv, dv=dv)
+    else:
+        x = rand_inputs(2, 120, 4, 2, d, dv=dv, seed=d + dv, dtype=dtype)
+        out, lse = attn(*(t.to(cuda) for t in x), 16, 48, scale=1.0, return_lse=True)
+        ro, rl = O.kernel_rounding_reference(*x, 16, 48, scale=1.0)
+        fo, fl = O.reference_simplicial(*(t.float() for t in x), 16, 48, scale=1.0, return_lse=True)
+        full = [p for p in range(120) if min(p + 1, 16) * min(p + 1, 48) >= 64]
+        e1 = assert_out_close(out[:, full], ro[:, full], dtype, atol=4e-3, rtol=2.0 ** -7)
+        e2 = assert_lse_close(lse, rl, dtype, rtol=1e-4)
+        e3 = assert_out_close(out, fo, dtype, atol=4e-2)
+        e4 = assert_lse_close(lse, fl, dtype, rtol=4e-3)
+        print(f"[mfma padded] d{d} dv{dv} bf16: vs rounding oracle out {e1:.2e} lse {e2:.2e}; "
+              f"vs fp32 oracle out {e3:.2e} lse {e4:.2e}", flush=True)
+    lengths = [7, 60, 33]
+    cu = torch.tensor([0, 7, 67, 100], dtype=torch.int32)
+    xv = rand_inputs(1, sum(lengths), 4, 2, d, dv=dv, seed=d * dv, dtype=dtype)
+    out, lse = varlen(*(v[0].to(cuda) for v in xv), cu.to(cuda), 8, 40, scale=1.0, return_lse=True)
+    ref_o, ref_l = O.varlen_reference(*(v[0].float() for v in xv), cu, 8, 40, scale=1.0, return_lse=True)
+    assert out.shape[-1] == dv
+    assert_out_close(out, ref_o, dtype, atol=4e-2 if dtype == torch.bfloat16 else None)
+    assert_lse_close(lse, ref_l, dtype, rtol=1e-2 if dtype == torch.bfloat16 else None)
+
+
 def test_zz_report_few_pair_lse_error(cuda):
     """The measured maximum of the LSE error at positions whose windows hold
     fewer than 64 pairs (bound 1e-2 there, 1e-3 elsewhere), over every bf16
