@@ -50,7 +50,7 @@ def _args():
     ap.add_argument("--decode-steps", type=int, default=200)
     ap.add_argument("--bwd-steps", type=int, default=10)
     ap.add_argument("--bwd-configs", default="C3,C4", help="further workloads of the backward leg")
-    ap.add_argument("--legs", default="prefill,configs,decode,global,fp32,backward,cpu")
+    ap.add_argument("--legs", default="prefill,configs,decode,global,fp32,backward,det,cpu")
     ap.add_argument("--configs", default="C2,C3,C4", help="prefill configurations of the configs leg")
     ap.add_argument("--workload", default="NS", help="prefill workload: NS, C2, C3, C4")
     ap.add_argument("--cpu-positions", type=int, default=256)
@@ -347,6 +347,33 @@ def backward_leg(args, fwd_ms, workload=None, cfg=None):
     }
 
 
+def determinant_leg(args):
+    """Score width 512 over value width 256 (the determinant expansion of
+    256-wide heads, simplicial_attention.py:111-148) at C4 geometry, bf16
+    forward on the matrix cores; FLOPs 2 * (DS + DV) per pair and head."""
+    import dataclasses
+    import torch
+    from archlab_amd import simplicial_attention
+    from archlab_amd import workloads as W
+    cfg = dataclasses.replace(W.C4, name="C4-DS512-DV256")
+    dev = torch.device("cuda:0")
+    g = torch.Generator("cpu").manual_seed(cfg.seed)
+    shp = lambda h, d: (cfg.batch, cfg.seqlen, h, d)  # noqa: E731
+    q = (torch.randn(shp(cfg.heads_q, 512), generator=g) * 0.5 / math.sqrt(512)).to(torch.bfloat16).to(dev)
+    k1, k2 = ((torch.randn(shp(cfg.heads_kv, 512), generator=g) * 0.5).to(torch.bfloat16).to(dev) for _ in range(2))
+    v1, v2 = ((torch.randn(shp(cfg.heads_kv, 256), generator=g) * 0.5).to(torch.bfloat16).to(dev) for _ in range(2))
+    fn = lambda: simplicial_attention(q, k1, k2, v1, v2, cfg.w2, cfg.w1, scale=1.0, return_lse=True,  # noqa: E731
+                                      kernel="mfma")
+    mean_ms, _, _ = _time_kernel(fn, max(5, args.steps // 5), 2)
+    flops = 2.0 * cfg.batch * cfg.heads_q * cfg.seqlen * cfg.w1 * cfg.w2 * (512 + 256)
+    del q, k1, k2, v1, v2
+    torch.cuda.empty_cache()
+    return {"workload": f"{cfg.name}: bf16 prefill B={cfg.batch} H={cfg.heads_q} S={cfg.seqlen} DS=512 DV=256 "
+                        f"w1(long)={cfg.w1} w2(short)={cfg.w2}", "ms_per_step": round(mean_ms, 4),
+            "flops_per_step": flops, "tflops": round(flops / (mean_ms * 1e-3) / 1e12, 2),
+            "kernel": "prefill_mfma_kernel<512,256>"}
+
+
 def copy_leg(args):
     """Plain device copy of a known byte count (1 GiB read + 1 GiB written per
     call): the calibration kernel for the FETCH_SIZE / WRITE_SIZE counters."""
@@ -518,6 +545,9 @@ def main():
             _progress(f"backward {name}: {b['bwd_ms']:.2f} ms")
         if extra:
             out["backward_configs"] = extra
+    if "det" in legs:
+        out["determinant_ds512"] = determinant_leg(args)
+        _progress(f"DS 512 / DV 256: {out['determinant_ds512']['ms_per_step']} ms")
     if "copy" in legs:
         out["copy_calibration"] = copy_leg(args)
     if "cpu" in legs:

@@ -125,10 +125,10 @@ static bool mfma_prefill_ok(const sa_prefill_args* a) {
            a->workspace_bytes >= prefill_f32_workspace_bytes(a);
   if (a->dtype != SA_DTYPE_BF16) return false;
   // score width DK, value width DV: DK == DV in {64, 128, 256}, or DK == 2 DV
-  // in {128, 256} (the determinant-score expansion of DV = 64 / 128)
+  // in {128, 256, 512} (the determinant-score expansion of DV = 64 / 128 / 256)
   const int dk = a->head_dim, dv = a->value_dim;
   const bool same = dk == dv && (dk == 64 || dk == 128 || dk == 256);
-  const bool expanded = (dk == 128 && dv == 64) || (dk == 256 && dv == 128);
+  const bool expanded = (dk == 128 && dv == 64) || (dk == 256 && dv == 128) || (dk == 512 && dv == 256);
   if (!same && !expanded) return false;
   const int64_t st[] = {a->q_stride_t, a->q_stride_h, a->k_stride_t, a->k_stride_h,
                         a->v_stride_t, a->v_stride_h, a->o_stride_t, a->o_stride_h};

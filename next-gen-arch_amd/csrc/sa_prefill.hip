@@ -35,8 +35,8 @@
 
 namespace sa {
 
-// A k1 row of zeros (widths up to 256) for A rows outside the short window.
-static __device__ __align__(16) const uint32_t kZeroRow[128] = {};
+// A k1 row of zeros (score widths up to 512) for A rows outside the short window.
+static __device__ __align__(16) const uint32_t kZeroRow[256] = {};
 
 struct PrefillParams {
   const void* q;   // bf16, or fp32 (F32 kernels)
@@ -77,7 +77,9 @@ constexpr int kPrefillChunkPF = 2;
 // k2, v2 and v1 arrive as rows of hi and lo terms, P is split the same way,
 // and every product runs on three term pairs; the output is fp32.
 template <int DK, int DV, int NQ, int NH, bool F32 = false>
-__global__ __launch_bounds__(64 * NQ * NH, (DK >= 256 || DV >= 256 ? 2 : (F32 ? 2 : kPrefillWavesPerSimd)))
+// (score width 512, the determinant expansion of 256-wide heads: one wave per
+// SIMD, the whole register file for 32 A fragments and 8 accumulator tiles)
+__global__ __launch_bounds__(64 * NQ * NH, (DK >= 512 ? 1 : (DK >= 256 || DV >= 256 ? 2 : (F32 ? 2 : kPrefillWavesPerSimd))))
 void prefill_mfma_kernel(PrefillParams p) {
   static_assert(NQ * NH == 4, "4 (token, head) pairs per block");
   constexpr int NW = NQ * NH;
@@ -268,8 +270,12 @@ void prefill_mfma_kernel(PrefillParams p) {
       else {
         // lanes outside the window read a row of zeros (A = 0 without a mask)
         const bf16* k1row = row_ok ? (const bf16*)p.k1 + k1off : (const bf16*)kZeroRow;
-        const auto ain = RB::load_a((const bf16*)p.q + qoff, k1row, half);
-        rb.make_a(ain, true, p.q_neg != 0);
+        if constexpr (DK >= 512) {
+          rb.form_a_grouped((const bf16*)p.q + qoff, k1row, half, p.q_neg != 0);
+        } else {
+          const auto ain = RB::load_a((const bf16*)p.q + qoff, k1row, half);
+          rb.make_a(ain, true, p.q_neg != 0);
+        }
       }
     }
     rb.reset(row_ok);
@@ -574,6 +580,7 @@ hipError_t launch_prefill_mfma(const sa_prefill_args* a, hipStream_t stream) {
   }
   if (dk == 128 && dv == 64) return dispatch_prefill_mfma_d<128, 64>(p, stream);
   if (dk == 256 && dv == 128) return dispatch_prefill_mfma_d<256, 128>(p, stream);
+  if (dk == 512 && dv == 256) return dispatch_prefill_mfma_d<512, 256>(p, stream);
   return hipErrorInvalidValue;
 }
 

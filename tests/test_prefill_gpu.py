@@ -121,7 +121,7 @@ def test_mfma_window_edges(cuda, ws, wl):
     _check(cuda, 1, 300, 4, 2, 128, ws, wl, torch.bfloat16, seed=ws * 7 + wl, kernel="mfma")
 
 
-@pytest.mark.parametrize("d,dv", [(128, 64), (256, 128)])
+@pytest.mark.parametrize("d,dv", [(128, 64), (256, 128), (512, 256)])
 @pytest.mark.parametrize("hq,hk", [(4, 4), (8, 2), (3, 1)])
 def test_mfma_score_and_value_widths_differ(cuda, d, dv, hq, hk):
     """Score width DK != value width DV (the determinant expansion's DK = 2 DV) on the MFMA kernel."""
@@ -132,6 +132,8 @@ def test_mfma_score_and_value_widths_differ(cuda, d, dv, hq, hk):
 def test_mfma_score_and_value_widths_differ_windows(cuda, ws, wl):
     _check(cuda, 1, 320, 4, 2, 128, ws, wl, torch.bfloat16, seed=ws + wl, kernel="mfma", dv=64)
     _check(cuda, 1, 200, 8, 2, 256, ws, wl, torch.bfloat16, seed=ws + wl + 1, kernel="mfma", dv=128)
+    # score width 512 (the determinant expansion of 256-wide heads), one wave per SIMD
+    _check(cuda, 1, 160, 4, 2, 512, ws, wl, torch.bfloat16, seed=ws + wl + 2, kernel="mfma", dv=256)
 
 
 def test_mfma_score_and_value_widths_differ_varlen(cuda):
