@@ -1453,16 +1453,11 @@ __global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_
   }
 }
 
-template <int DK, int DV, int NR, bool PH, bool F32 = false>
+template <int DK, int DV, int NR, bool PH, bool F32, int NWK>
 hipError_t launch_dkv2_t(const BwdParams& p, hipStream_t stream) {
   constexpr int EW = F32 ? 2 : 1;
   constexpr int RSA = 2 * EW * DK + 32, RSB = 2 * EW * DV + 32, RKV = 2 * EW * (DK + DV);
   constexpr int SS = (2 * RKV + 1023) / 1024 * 1024;  // stage slot
-  // one 8-wave workgroup per CU when both widths are 128, 4-wave workgroups
-  // otherwise (a wave forms 32 / NWK rows per step in whole 64-lane
-  // instructions; at DK = 256 the 4 waves hold one workgroup per CU; fp32
-  // inputs: 4 waves, one per SIMD, for the hi/lo fragments)
-  constexpr int NWK = DK == 128 && DV == 128 && !F32 ? 8 : 4;
   const size_t lds = (size_t)2 * NR * 32 * (RSA + RSB) + (size_t)64 * NR * RKV + 3 * SS + (size_t)NWK * 64 * 16;
   const int nblocks = (p.tokens + 32 * NWK - 1) / (32 * NWK) * p.hk;
   // more short-key rows than one launch's LDS holds: two launches (phases 1, 2)
@@ -1479,14 +1474,32 @@ hipError_t launch_dkv2_t(const BwdParams& p, hipStream_t stream) {
   return hipSuccess;
 }
 
+// Keys per workgroup (32 per wave, NWK waves): 8 waves when both widths are
+// 128 (bf16), 4 otherwise (at DK = 256 and for fp32 the 4 waves fill a CU's
+// LDS or registers).  When 8-wave workgroups would leave CUs without work --
+// few KV heads over few tokens, e.g. the reference adapter's 2 KV heads x
+// 16K tokens: 128 workgroups of 256 keys for 256 CUs -- 4-wave ones run
+// (adapter shape: fwd + bwd 12.0 against 12.8 ms).  Narrower still measured
+// slower (14.8 ms): every workgroup forms all 32 A / B rows of each step, so
+// that work grows with the workgroup count, and one wave per SIMD hides less.
+template <int DK, int DV, int NR, bool PH, bool F32 = false>
+hipError_t launch_dkv2_w(const BwdParams& p, hipStream_t stream) {
+  if constexpr (DK == 128 && DV == 128 && !F32) {
+    const int64_t cus = device_cu_count();
+    const int64_t blocks8 = (int64_t)(p.tokens + 255) / 256 * p.hk;
+    if (blocks8 >= (NR == 1 ? 2 : 1) * cus) return launch_dkv2_t<DK, DV, NR, PH, F32, 8>(p, stream);
+  }
+  return launch_dkv2_t<DK, DV, NR, PH, F32, 4>(p, stream);
+}
+
 template <int DK, int DV>
 hipError_t launch_dkv2_d(const BwdParams& p, hipStream_t stream) {
   if constexpr (DK > 128) {
-    return launch_dkv2_t<DK, DV, 1, true>(p, stream);  // LDS for one row group per launch
+    return launch_dkv2_w<DK, DV, 1, true>(p, stream);  // LDS for one row group per launch
   } else {
-    if (p.ws <= 32) return launch_dkv2_t<DK, DV, 1, false>(p, stream);
-    if (p.ws <= 64) return launch_dkv2_t<DK, DV, 2, false>(p, stream);
-    return launch_dkv2_t<DK, DV, 2, true>(p, stream);  // two launches of two row groups
+    if (p.ws <= 32) return launch_dkv2_w<DK, DV, 1, false>(p, stream);
+    if (p.ws <= 64) return launch_dkv2_w<DK, DV, 2, false>(p, stream);
+    return launch_dkv2_w<DK, DV, 2, true>(p, stream);  // two launches of two row groups
   }
 }
 
@@ -1565,7 +1578,7 @@ hipError_t launch_bwd_dk1_sum(const BwdParams& p, hipStream_t stream) {
 hipError_t launch_bwd_dkv2_mfma(const BwdParams& p, hipStream_t stream) {
   if (p.f32) {  // fp32: one 32-row group of short keys
     if (!bwd_mfma_ok(p) || p.ws > 32) return hipErrorNotSupported;
-    return p.d == 64 ? launch_dkv2_t<64, 64, 1, false, true>(p, stream) : launch_dkv2_t<128, 128, 1, false, true>(p, stream);
+    return p.d == 64 ? launch_dkv2_w<64, 64, 1, false, true>(p, stream) : launch_dkv2_w<128, 128, 1, false, true>(p, stream);
   }
   // one launch covers 64 short keys (32 at DK = 256); two launches over the fp32 partial twice that
   const int one = p.d > 128 ? 32 : 64;
