@@ -531,7 +531,8 @@ def main():
         fp32["DSV41_fwd_bwd"]["bwd_fp32_over_bf16"] = round(f32b["bwd_ms"] / b16b["bwd_ms"], 3)
         _progress(f"fp32 DSV41 fwd+bwd: {f32b['fwd_bwd_ms']:.2f} ms (bwd {f32b['bwd_ms']:.2f} ms, "
                   f"bf16 bwd {b16b['bwd_ms']:.2f} ms)")
-        _progress("fp32: " + ", ".join(f"{k} {v.get('ms_per_step', v.get('us_per_step'))}" for k, v in fp32.items()))
+        _progress("fp32: " + ", ".join(
+            f"{k} {v.get('ms_per_step', v.get('us_per_step', v.get('fwd_bwd_ms')))}" for k, v in fp32.items()))
     if fp32:
         out["fp32"] = fp32
     if "backward" in legs:

@@ -45,6 +45,10 @@ struct BwdParams {
   const bf16* k2s;
   const bf16* v2s;
   int f32;
+  // dk2 / dv2 walk splits (bwd_dkv2_plan): each split's fp32 sums over its
+  // part of the queries reaching a key, [splits][tokens][hk][max(D, DV)],
+  // added in split order by a second kernel; null with one split
+  float* dkv2s;
 };
 
 // Queries per dq workgroup (4 waves: NQ queries x NH = 4 / NQ heads of one KV
@@ -63,5 +67,15 @@ hipError_t launch_bwd_dkv2_mfma(const BwdParams& p, hipStream_t stream);
 bool bwd_dk1_fused_ok(const BwdParams& p);
 // dk1 = the fixed-order sum of the dq pass's partials (p.dk1p)
 hipError_t launch_bwd_dk1_sum(const BwdParams& p, hipStream_t stream);
+
+// MFMA dk2 / dv2 pass: waves per workgroup (32 long keys each) and walk
+// splits (pieces of each workgroup's walk over the queries, for shapes whose
+// (key block, KV head) workgroups leave CUs idle).  A function of the shape
+// and the device's CU count only, so that the workspace query and the launch
+// agree.
+struct Dkv2Plan {
+  int nwk, splits;
+};
+Dkv2Plan bwd_dkv2_plan(int tokens, int hk, int d, int dv, int ws, int wl, bool f32, int cus);
 
 }  // namespace sa

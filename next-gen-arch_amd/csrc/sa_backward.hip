@@ -583,8 +583,24 @@ static size_t dkv2_partial_bytes(const sa_prefill_bwd_args* a) {
     return 0;
   return ((size_t)f.total_tokens * f.heads_kv * (f.head_dim + f.value_dim) * sizeof(float) + 255) & ~(size_t)255;
 }
+// bf16 dk2 / dv2 on the matrix cores in one launch (widths 64 / 128, short
+// window <= 64) whose plan cuts the walks into pieces: the pieces' fp32 sums,
+// [splits][tokens][hk][max(D, DV)] (dk2's, then, reused, dv2's)
+static size_t dkv2_split_bytes(const sa_prefill_bwd_args* a) {
+  const sa_prefill_args& f = a->fwd;
+  const bool narrow = (f.head_dim == 64 || f.head_dim == 128) && (f.value_dim == 64 || f.value_dim == 128);
+  if (f.dtype != SA_DTYPE_BF16 || (f.flags & SA_FLAG_FORCE_GENERIC) || !narrow || f.short_window > 64 ||
+      f.heads_kv <= 0)
+    return 0;
+  const Dkv2Plan pl = bwd_dkv2_plan(f.total_tokens, f.heads_kv, f.head_dim, f.value_dim, f.short_window,
+                                    f.long_window, false, device_cu_count());
+  if (pl.splits <= 1) return 0;
+  const size_t w = (size_t)(f.head_dim > f.value_dim ? f.head_dim : f.value_dim);
+  return ((size_t)pl.splits * f.total_tokens * f.heads_kv * w * sizeof(float) + 255) & ~(size_t)255;
+}
 size_t prefill_bwd_workspace_bytes(const sa_prefill_bwd_args* a) {
-  return 2 * bwd_row_bytes(a) + dk1_partial_bytes(a) + dkv2_partial_bytes(a) + 2 * f32_split_bytes(a);
+  return 2 * bwd_row_bytes(a) + dk1_partial_bytes(a) + dkv2_partial_bytes(a) + 2 * f32_split_bytes(a) +
+         dkv2_split_bytes(a);
 }
 
 template <typename T>
@@ -702,6 +718,9 @@ hipError_t launch_prefill_bwd(const sa_prefill_bwd_args* a, void* ws, hipStream_
   }
   if (dk1_partial_bytes(a) && bwd_dk1_fused_ok(p)) p.dk1p = (float*)((char*)ws + 2 * bwd_row_bytes(a));
   if (dkv2_partial_bytes(a)) p.dkv2p = (float*)((char*)ws + 2 * bwd_row_bytes(a) + dk1_partial_bytes(a));
+  if (dkv2_split_bytes(a))
+    p.dkv2s = (float*)((char*)ws + 2 * bwd_row_bytes(a) + dk1_partial_bytes(a) + dkv2_partial_bytes(a) +
+                       2 * f32_split_bytes(a));
   if (f.dtype == SA_DTYPE_F32) return launch_bwd_t<float>(p, stream);
   return launch_bwd_t<bf16>(p, stream);
 }

@@ -43,6 +43,9 @@ constexpr int kDqPF = 1;    // dq pass
 constexpr int kDk1PF = 1;   // dk1 / dv1 pass (dv1 reads two ahead)
 constexpr int kDkv2PF = 2;  // dk2 / dv2 pass
 
+constexpr size_t kLdsPerCu = 160 * 1024;  // gfx950
+constexpr int kMaxWalkSplits = 8;         // dk2 / dv2 walk pieces per (key block, KV head)
+
 // Wave-level tile products used by the backward passes (D = head dim).
 template <int D>
 struct BwdOps {
@@ -1010,9 +1013,13 @@ __global__ __launch_bounds__(256) void bwd_dk1_sum_kernel(BwdParams p, int qbloc
 // hi/lo rows (hi and lo fragments), fp32 q / dout / k1 / v1 rows in the
 // stage and the ring, A / B tile rows formed as [hi: D | lo: D] from fp32
 // products, three term pairs per product, fp32 output.
+// splits > 1 (one launch, bf16): the workgroups of a (key block, KV head)
+// walk contiguous pieces of its queries and write fp32 sums to p.dkv2s
+// ([split][tokens][hk][XW]); bwd_dkv2_sum_kernel adds them in split order.
 template <int DK, int DV, int MODE, int NWK, int NR, bool PH, bool F32 = false>
 __global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_mfma_kernel(BwdParams p,
-                                                                                           int nblocks, int phase) {
+                                                                                           int nblocks, int phase,
+                                                                                           int splits) {
   static_assert(!F32 || (DK == DV && DK <= 128 && NR == 1 && !PH), "fp32 inputs: equal widths up to 128, one group");
   constexpr bool kDK = MODE == 1, kDV = MODE == 2;
   constexpr int EW = F32 ? 2 : 1;  // bf16 units per element of an LDS row
@@ -1044,10 +1051,14 @@ __global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_
   floatx4* const scal = (floatx4*)(stage + 3 * SS) + 64 * wid;
   constexpr bool kPhased = PH;
   const int r0 = kPhased && phase == 2 ? NR : 0;  // row group offset of this launch (the ring holds 64 NR rows)
+  // walk splits: bf16 single launches only (the launcher passes 1 otherwise)
+  constexpr bool kSplit = !PH && !F32;
+  const int nsplit = kSplit ? splits : 1;
   const int lb = xcd_remap(bid_x(), nblocks);
   const int kblocks = (p.tokens + KB - 1) / KB;
   const int kb = lb % kblocks;
-  const int g = lb / kblocks;
+  const int g = kSplit ? lb / kblocks % p.hk : lb / kblocks;
+  const int split = kSplit ? lb / kblocks / p.hk : 0;
   const int k0 = kb * KB;
   const int last = p.tokens - 1;
   const int kw = k0 + 32 * wid + n;  // this lane's key (column of the C layout)
@@ -1095,10 +1106,71 @@ __global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_
       }
   }
 
+  // the queries reaching the block's keys, t = k0 .. min(last, k0 + KB + wl - 2),
+  // cut into `splits` contiguous pieces; this workgroup walks piece `split`
+  const int walk = min(last, k0 + KB - 1 + p.wl - 1) - k0 + 1;
+  const int tfirst = k0 + (int)((int64_t)walk * split / nsplit);
+  const int tlast = k0 + (int)((int64_t)walk * (split + 1) / nsplit) - 1;
   // step s <-> (t = tfirst + s / G, h = g*G + s % G)
-  const int tfirst = k0;
-  const int tlast = min(last, k0 + KB - 1 + p.wl - 1);
   const int nsteps = (tlast - tfirst + 1) * G;
+  // write: acc[db] holds d = 32*db + acc_row(r, half) of key kw
+  auto write_out = [&]() {
+    if (!kvalid) return;
+    if (kSplit && nsplit > 1) {
+      float* part = p.dkv2s + (((int64_t)split * p.tokens + kw) * p.hk + g) * XW;
+#pragma unroll
+      for (int db = 0; db < XW / 32; ++db)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          floatx4 x;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[e] = acc[db][4 * q4 + e];
+          *(floatx4*)(part + 32 * db + 8 * q4 + 4 * half) = x;
+        }
+    } else if (kPhased && phase == 1) {
+      float* part = part_row();
+#pragma unroll
+      for (int db = 0; db < XW / 32; ++db)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          floatx4 x;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[e] = acc[db][4 * q4 + e];
+          *(floatx4*)(part + 32 * db + 8 * q4 + 4 * half) = x;
+        }
+    } else if (F32) {
+      float* orow = kDK ? (float*)p.dk2 + (int64_t)kw * p.dk_st + (int64_t)g * p.dk_sh
+                        : (float*)p.dv2 + (int64_t)kw * p.dv_st + (int64_t)g * p.dv_sh;
+#pragma unroll
+      for (int db = 0; db < XW / 32; ++db)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          floatx4 a;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a[e] = acc[db][4 * q4 + e];
+          *(floatx4*)(orow + 32 * db + 8 * q4 + 4 * half) = a;
+        }
+    } else {
+      bf16* orow = kDK ? (bf16*)p.dk2 + (int64_t)kw * p.dk_st + (int64_t)g * p.dk_sh
+                       : (bf16*)p.dv2 + (int64_t)kw * p.dv_st + (int64_t)g * p.dv_sh;
+#pragma unroll
+      for (int db = 0; db < XW / 32; ++db)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int d = 32 * db + 8 * q4 + 4 * half;
+          bf16x4 a;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a[e] = (bf16)acc[db][4 * q4 + e];
+          *(bf16x4*)(orow + d) = a;
+        }
+    }
+  };
+  // an empty piece (a short last key block): zero sums (uniform, before any
+  // barrier); one piece always holds t = k0
+  if (kSplit && nsteps <= 0) {
+    write_out();
+    return;
+  }
 
   // Step st <-> (t = tfirst + st / G, h = g*G + st % G), stage slot st % 3:
   // carried from step to step (no divisions in the step loop).
@@ -1413,60 +1485,62 @@ __global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_
     }
   }
 
-  // write: acc[db] holds d = 32*db + acc_row(r, half) of key kw
-  if (kPhased && phase == 1 && kvalid) {
-    float* part = part_row();
+  write_out();
+}
+
+// dk2 or dv2 (mode 1 / 2) = the sum of the walk splits' fp32 sums in split
+// order; 4 values per thread
+template <int XW>
+__global__ __launch_bounds__(256) void bwd_dkv2_sum_kernel(BwdParams p, int splits, int mode) {
+  const int64_t i = (int64_t)bid_x() * 256 + tid_x();
+  const int64_t rows = (int64_t)p.tokens * p.hk;
+  if (i >= rows * (XW / 4)) return;
+  const int64_t row = i / (XW / 4);
+  const int c = (int)(i % (XW / 4)) * 4;
+  const float* src = p.dkv2s + row * XW + c;
+  floatx4 acc = *(const floatx4*)src;
+  for (int k = 1; k < splits; ++k) {
+    const floatx4 x = *(const floatx4*)(src + (int64_t)k * rows * XW);
 #pragma unroll
-    for (int db = 0; db < XW / 32; ++db)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        floatx4 x;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) x[e] = acc[db][4 * q4 + e];
-        *(floatx4*)(part + 32 * db + 8 * q4 + 4 * half) = x;
-      }
-  } else if (F32 && kvalid) {
-    float* orow = kDK ? (float*)p.dk2 + (int64_t)kw * p.dk_st + (int64_t)g * p.dk_sh
-                      : (float*)p.dv2 + (int64_t)kw * p.dv_st + (int64_t)g * p.dv_sh;
-#pragma unroll
-    for (int db = 0; db < XW / 32; ++db)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        floatx4 a;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) a[e] = acc[db][4 * q4 + e];
-        *(floatx4*)(orow + 32 * db + 8 * q4 + 4 * half) = a;
-      }
-  } else if (kvalid) {
-    bf16* orow = kDK ? (bf16*)p.dk2 + (int64_t)kw * p.dk_st + (int64_t)g * p.dk_sh
-                     : (bf16*)p.dv2 + (int64_t)kw * p.dv_st + (int64_t)g * p.dv_sh;
-#pragma unroll
-    for (int db = 0; db < XW / 32; ++db)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int d = 32 * db + 8 * q4 + 4 * half;
-        bf16x4 a;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) a[e] = (bf16)acc[db][4 * q4 + e];
-        *(bf16x4*)(orow + d) = a;
-      }
+    for (int e = 0; e < 4; ++e) acc[e] += x[e];
   }
+  const int64_t t = row / p.hk, g = row % p.hk;
+  bf16* o = mode == 1 ? (bf16*)p.dk2 + t * p.dk_st + g * p.dk_sh : (bf16*)p.dv2 + t * p.dv_st + g * p.dv_sh;
+  bf16x4 b;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) b[e] = (bf16)acc[e];
+  *(bf16x4*)(o + c) = b;
+}
+
+// LDS bytes of a dk2 / dv2 workgroup (EW: bf16 units per row element)
+constexpr size_t dkv2_lds_bytes(int dk, int dv, int nr, int nwk, int ew) {
+  const size_t rsa = 2 * ew * dk + 32, rsb = 2 * ew * dv + 32, rkv = 2 * ew * (dk + dv);
+  const size_t ss = (2 * rkv + 1023) / 1024 * 1024;  // stage slot
+  return 2 * nr * 32 * (rsa + rsb) + 64 * nr * rkv + 3 * ss + (size_t)nwk * 64 * 16;
 }
 
 template <int DK, int DV, int NR, bool PH, bool F32, int NWK>
-hipError_t launch_dkv2_t(const BwdParams& p, hipStream_t stream) {
-  constexpr int EW = F32 ? 2 : 1;
-  constexpr int RSA = 2 * EW * DK + 32, RSB = 2 * EW * DV + 32, RKV = 2 * EW * (DK + DV);
-  constexpr int SS = (2 * RKV + 1023) / 1024 * 1024;  // stage slot
-  const size_t lds = (size_t)2 * NR * 32 * (RSA + RSB) + (size_t)64 * NR * RKV + 3 * SS + (size_t)NWK * 64 * 16;
-  const int nblocks = (p.tokens + 32 * NWK - 1) / (32 * NWK) * p.hk;
+hipError_t launch_dkv2_t(const BwdParams& p, int splits, hipStream_t stream) {
+  constexpr size_t lds = dkv2_lds_bytes(DK, DV, NR, NWK, F32 ? 2 : 1);
   // more short-key rows than one launch's LDS holds: two launches (phases 1, 2)
   const bool two = PH && p.ws > 32 * NR;
-  for (auto kern : {bwd_dkv2_mfma_kernel<DK, DV, 1, NWK, NR, PH, F32>, bwd_dkv2_mfma_kernel<DK, DV, 2, NWK, NR, PH, F32>}) {
+  if (two || F32 || !p.dkv2s) splits = 1;
+  const int nblocks = (p.tokens + 32 * NWK - 1) / (32 * NWK) * p.hk * splits;
+  for (int mode = 1; mode <= 2; ++mode) {
+    auto kern = mode == 1 ? bwd_dkv2_mfma_kernel<DK, DV, 1, NWK, NR, PH, F32>
+                          : bwd_dkv2_mfma_kernel<DK, DV, 2, NWK, NR, PH, F32>;
     hipError_t e = set_lds_limit((const void*)kern, lds);
     if (e != hipSuccess) return e;
     for (int phase = two ? 1 : 0; phase <= (two ? 2 : 0); ++phase) {
-      hipLaunchKernelGGL(kern, dim3(nblocks), dim3(64 * NWK), lds, stream, p, nblocks, phase);
+      hipLaunchKernelGGL(kern, dim3(nblocks), dim3(64 * NWK), lds, stream, p, nblocks, phase, splits);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
+    if (splits > 1) {
+      const int xw = mode == 1 ? DK : DV;
+      const dim3 grid((unsigned)(((int64_t)p.tokens * p.hk * (xw / 4) + 255) / 256));
+      if (xw == 64) hipLaunchKernelGGL(bwd_dkv2_sum_kernel<64>, grid, dim3(256), 0, stream, p, splits, mode);
+      else hipLaunchKernelGGL(bwd_dkv2_sum_kernel<128>, grid, dim3(256), 0, stream, p, splits, mode);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
     }
@@ -1474,22 +1548,13 @@ hipError_t launch_dkv2_t(const BwdParams& p, hipStream_t stream) {
   return hipSuccess;
 }
 
-// Keys per workgroup (32 per wave, NWK waves): 8 waves when both widths are
-// 128 (bf16), 4 otherwise (at DK = 256 and for fp32 the 4 waves fill a CU's
-// LDS or registers).  When 8-wave workgroups would leave CUs without work --
-// few KV heads over few tokens, e.g. the reference adapter's 2 KV heads x
-// 16K tokens: 128 workgroups of 256 keys for 256 CUs -- 4-wave ones run
-// (adapter shape: fwd + bwd 12.0 against 12.8 ms).  Narrower still measured
-// slower (14.8 ms): every workgroup forms all 32 A / B rows of each step, so
-// that work grows with the workgroup count, and one wave per SIMD hides less.
 template <int DK, int DV, int NR, bool PH, bool F32 = false>
 hipError_t launch_dkv2_w(const BwdParams& p, hipStream_t stream) {
+  const Dkv2Plan pl = bwd_dkv2_plan(p.tokens, p.hk, DK, DV, p.ws, p.wl, F32, device_cu_count());
   if constexpr (DK == 128 && DV == 128 && !F32) {
-    const int64_t cus = device_cu_count();
-    const int64_t blocks8 = (int64_t)(p.tokens + 255) / 256 * p.hk;
-    if (blocks8 >= (NR == 1 ? 2 : 1) * cus) return launch_dkv2_t<DK, DV, NR, PH, F32, 8>(p, stream);
+    if (pl.nwk == 8) return launch_dkv2_t<DK, DV, NR, PH, F32, 8>(p, pl.splits, stream);
   }
-  return launch_dkv2_t<DK, DV, NR, PH, F32, 4>(p, stream);
+  return launch_dkv2_t<DK, DV, NR, PH, F32, 4>(p, pl.splits, stream);
 }
 
 template <int DK, int DV>
@@ -1516,7 +1581,12 @@ bool bwd_mfma_ok(const BwdParams& p) {
     if (s % 8) return false;
   const uintptr_t ptrs = (uintptr_t)p.q | (uintptr_t)p.k1 | (uintptr_t)p.k2 | (uintptr_t)p.v1 |
                          (uintptr_t)p.v2 | (uintptr_t)p.dout;
-  return (ptrs & 15) == 0;
+  // gradients are written 4 elements at a time
+  const int64_t ost[] = {p.dq_st, p.dq_sh, p.dk_st, p.dk_sh, p.dv_st, p.dv_sh};
+  for (int64_t s : ost)
+    if (s % 4) return false;
+  const uintptr_t optrs = (uintptr_t)p.dq | (uintptr_t)p.dk1 | (uintptr_t)p.dk2 | (uintptr_t)p.dv1 | (uintptr_t)p.dv2;
+  return (ptrs & 15) == 0 && (optrs & 15) == 0;
 }
 
 // fn(DK, DV) with the widths as integral constants; WIDE: DK = 256 as well
@@ -1540,6 +1610,33 @@ BwdGeo base_geo(const BwdParams& p) {
 }
 
 }  // namespace
+
+// Keys per workgroup (32 per wave, NWK waves): 8 waves when both widths are
+// 128 (bf16), 4 otherwise (at DK = 256 and for fp32 the 4 waves fill a CU's
+// LDS or registers).  When 8-wave workgroups would leave CUs without work --
+// few KV heads over few tokens, e.g. the reference adapter's 2 KV heads x
+// 16K tokens: 128 workgroups of 256 keys for 256 CUs -- 4-wave ones run, and
+// at bf16 widths <= 128 with one launch (short window <= 64) each (key block,
+// KV head) walk is cut into as many pieces as fill the CUs' resident
+// workgroup slots (two waves per SIMD, or what the LDS allows), up to 8 and
+// at least 128 queries per piece: the pieces' fp32 sums are added in a fixed
+// order.  Narrower workgroups alone measured slower (every workgroup forms
+// all 32 A / B rows of each step, so that work grows with the workgroup
+// count); a split walk forms each step's rows once, as before.
+Dkv2Plan bwd_dkv2_plan(int tokens, int hk, int d, int dv, int ws, int wl, bool f32, int cus) {
+  const int nr = ws <= 32 ? 1 : 2;  // row groups per launch at widths <= 128
+  const int64_t blocks8 = (int64_t)(tokens + 255) / 256 * hk;
+  if (!f32 && d == 128 && dv == 128 && blocks8 >= (nr == 1 ? 2 : 1) * (int64_t)cus) return {8, 1};
+  constexpr int nwk = 4;
+  if (f32 || d > 128 || dv > 128 || ws > 64 || tokens <= 0 || hk <= 0) return {nwk, 1};
+  const int64_t blocks = (int64_t)(tokens + 32 * nwk - 1) / (32 * nwk) * hk;
+  const int64_t by_lds = (int64_t)kLdsPerCu / dkv2_lds_bytes(d, dv, nr, nwk, 1);
+  const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(by_lds, 8 / nwk));
+  int64_t splits = ((int64_t)cus * per_cu + blocks - 1) / blocks;
+  splits = std::min<int64_t>(splits, kMaxWalkSplits);
+  splits = std::min<int64_t>(splits, ((int64_t)32 * nwk + wl - 1) / 128);  // pieces of >= 128 queries
+  return {nwk, (int)std::max<int64_t>(splits, 1)};
+}
 
 hipError_t launch_bwd_dq_mfma(const BwdParams& p, hipStream_t stream) {
   if (!bwd_mfma_ok(p)) return hipErrorNotSupported;

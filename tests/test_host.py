@@ -372,17 +372,47 @@ def test_backward_workspace_reserves_dk1_partials_for_fused_shapes(dtype, hq, hk
     # k2 and v2 as hi/lo bf16 rows, [tokens][hk][2 d] each
     f32_mfma = dtype == "f32" and d == dv and d in (64, 128) and ws <= 32
     split = 2 * ((tokens * hk * d * 4 + 255) // 256 * 256) if f32_mfma else 0
-    assert lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args)) == 2 * rows + part + dkv2 + split
+    walk = _walk_split_bytes(dtype, tokens, hk, d, dv, ws, 512)
+    assert lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args)) == 2 * rows + part + dkv2 + split + walk
     if fused:
         # past 8 GiB of partials the separate dk1 pass runs: no partials reserved
         big = int((8 << 30) / per_query) // 4 * 4 + 8
         args.fwd.total_tokens = args.fwd.seqlen = big
         rows = (big * hq * 4 + 255) // 256 * 256
         split = 2 * ((big * hk * d * 4 + 255) // 256 * 256) if f32_mfma else 0
-        assert lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args)) == 2 * rows + split
+        walk = _walk_split_bytes(dtype, big, hk, d, dv, ws, 512)
+        assert lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args)) == 2 * rows + split + walk
     # a caller short of memory selects the separate dk1 pass: no partials reserved
     args.fwd.total_tokens = args.fwd.seqlen = tokens
     args.fwd.flags = _native.SA_FLAG_SEPARATE_DK1
     rows = (tokens * hq * 4 + 255) // 256 * 256
     split = 2 * ((tokens * hk * d * 4 + 255) // 256 * 256) if f32_mfma else 0
-    assert lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args)) == 2 * rows + dkv2 + split
+    walk = _walk_split_bytes(dtype, tokens, hk, d, dv, ws, 512)
+    assert lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args)) == 2 * rows + dkv2 + split + walk
+
+
+def _dkv2_lds(d, dv, nr, nwk):
+    rsa, rsb, rkv = 2 * d + 32, 2 * dv + 32, 2 * (d + dv)
+    return 2 * nr * 32 * (rsa + rsb) + 64 * nr * rkv + 3 * -(-2 * rkv // 1024) * 1024 + nwk * 64 * 16
+
+
+def _walk_split_bytes(dtype, tokens, hk, d, dv, ws, wl, cus=256):
+    """Workspace of the dk2 / dv2 walk splits (bf16, widths 64 / 128, short
+    window <= 64): when the (key block, KV head) workgroups -- 256 keys (8 waves)
+    if both widths are 128 and they make at least 2 (one group of 32 short rows)
+    or 1 (two groups) per CU, else 128 keys (4 waves) -- number fewer than the
+    CUs' resident slots (two waves per SIMD, or what 160 KB of LDS holds), each
+    walk over the queries is cut into pieces (up to 8, >= 128 queries each),
+    whose fp32 sums take [splits][tokens][hk][max(d, dv)].  Without a GPU the
+    library counts 256 CUs."""
+    if dtype != "bf16" or d not in (64, 128) or dv not in (64, 128) or ws > 64:
+        return 0
+    nr = 1 if ws <= 32 else 2
+    if d == dv == 128 and -(-tokens // 256) * hk >= (2 if nr == 1 else 1) * cus:
+        return 0
+    blocks = -(-tokens // 128) * hk
+    per_cu = max(1, min(160 * 1024 // _dkv2_lds(d, dv, nr, 4), 2))
+    splits = min(-(-cus * per_cu // blocks), 8, (128 + wl - 1) // 128)
+    if splits <= 1:
+        return 0
+    return (splits * tokens * hk * max(d, dv) * 4 + 255) // 256 * 256
