@@ -87,8 +87,9 @@ enum {
   SA_FLAG_FORCE_GENERIC = 1, /* use the portable (non-MFMA) kernel; for cross-checks */
   /* sa_prefill_bwd only: compute dk1 in a pass of its own instead of from
    * partials written by the dq pass.  The workspace then holds no dk1
-   * partials (those take 16-17.5x the bytes of q); the backward runs one
-   * more recomputation pass (about 20 % more time at the benchmark shape). */
+   * partials (those take 16-17.5x the bytes of q per 32 keys of short
+   * window); the backward runs one more recomputation pass (about 20 % more
+   * time at the benchmark shape). */
   SA_FLAG_SEPARATE_DK1 = 2
 };
 
@@ -186,13 +187,21 @@ typedef struct sa_prefill_bwd_args {
 } sa_prefill_bwd_args;
 
 /* Bytes of device workspace sa_prefill_bwd needs (256-byte aligned): two fp32
- * [tokens, heads_q] rows, plus the dq pass's dk1 partials where it produces
- * dk1 (bf16, head_dim and value_dim each 64 or 128, or head_dim 256 over
- * value_dim 128 / 256; short window <= 32; 16-17.5x the bytes of q, up to
- * 8 GiB; none with SA_FLAG_SEPARATE_DK1 in args->fwd.flags), plus, for
- * short windows of 65-128 (33-64 at head_dim 256), the fp32 dk2 and dv2 sums
- * of the first of two dk2 / dv2 launches ([tokens][heads_kv][head_dim +
- * value_dim]). */
+ * [tokens, heads_q] rows, plus
+ * - the dq pass's dk1 partials where it produces dk1 (bf16 with head_dim and
+ *   value_dim each 64 or 128, or head_dim 256 over value_dim 128 / 256, short
+ *   window <= 64; fp32 with head_dim == value_dim in {64, 128}, short window
+ *   <= 32): 16-17.5x the bytes of q per 32 keys of short window, up to 8 GiB;
+ *   none with SA_FLAG_SEPARATE_DK1 in args->fwd.flags;
+ * - for short windows of 65-128 (33-64 at head_dim 256), the fp32 dk2 and dv2
+ *   sums of the first of two dk2 / dv2 launches ([tokens][heads_kv][head_dim +
+ *   value_dim]);
+ * - for fp32 inputs on the matrix cores, k2 and v2 as hi/lo bf16 rows
+ *   ([tokens][heads_kv][2 head_dim] each);
+ * - for bf16 at widths 64 / 128 and short windows <= 64 whose (key block, KV
+ *   head) work leaves CUs idle (few KV heads over few tokens), the fp32 sums of
+ *   the dk2 / dv2 pass's walk pieces ([pieces <= 8][tokens][heads_kv]
+ *   [max(head_dim, value_dim)]). */
 size_t sa_prefill_bwd_workspace_bytes(const sa_prefill_bwd_args* args);
 
 /* Backward of sa_prefill_fwd: writes dq, dk1, dk2, dv1, dv2 (each exactly

@@ -31,9 +31,9 @@ struct BwdParams {
   float scale;
   int mfma;  // bf16 inputs and the MFMA passes allowed (not forced onto the portable kernels)
   // dk1 from the dq pass (bwd_dk1_fused_ok): per dq workgroup (NQ queries x
-  // NH heads of one KV group) the 31 + NQ short-key rows of Σ dA_{t,j} ⊙ q_{t,h},
-  // fp32 [hk * hsub][qblocks][31 + NQ][D], summed by bwd_dk1_sum_kernel;
-  // null: the separate dk1 pass
+  // NH heads of one KV group) and row group r of short keys, the 31 + NQ
+  // short-key rows of Σ dA_{t,j} ⊙ q_{t,h}, fp32 [hk * hsub][qblocks][nr]
+  // [31 + NQ][D], summed by bwd_dk1_sum_kernel; null: the separate dk1 pass
   float* dk1p;
   // Short windows of 65-128 keys (33-64 at score width 256): the dk2 / dv2
   // passes run as two launches and carry the first one's fp32 sums here,
@@ -62,8 +62,8 @@ hipError_t launch_bwd_dq_mfma(const BwdParams& p, hipStream_t stream);
 hipError_t launch_bwd_dkv1_mfma(const BwdParams& p, hipStream_t stream);
 hipError_t launch_bwd_dkv2_mfma(const BwdParams& p, hipStream_t stream);
 // The dq pass can produce dk1 (p.dk1p set): the MFMA passes apply and the
-// short window fits one 32-row group.  The MFMA dkv1 launch then computes dv1
-// only.
+// short window fits two 32-row groups (one for fp32 inputs).  The MFMA dkv1
+// launch then computes dv1 only.
 bool bwd_dk1_fused_ok(const BwdParams& p);
 // dk1 = the fixed-order sum of the dq pass's partials (p.dk1p)
 hipError_t launch_bwd_dk1_sum(const BwdParams& p, hipStream_t stream);

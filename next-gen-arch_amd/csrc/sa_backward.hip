@@ -555,9 +555,9 @@ static bool dk1_fused_shape(const sa_prefill_bwd_args* a) {
   if (f.flags & SA_FLAG_SEPARATE_DK1) return false;
   if (f.dtype == SA_DTYPE_F32) return f32_mfma_shape(f) && f.heads_kv > 0;
   return f.dtype == SA_DTYPE_BF16 && !(f.flags & SA_FLAG_FORCE_GENERIC) && (narrow || wide) &&
-         f.short_window <= 32 && f.heads_kv > 0;
+         f.short_window <= 64 && f.heads_kv > 0;
 }
-// The partials take 16-17.5x the bytes of q; past kDk1PartialCap (or with
+// The partials take 16-17.5x the bytes of q per row group; past kDk1PartialCap (or with
 // SA_FLAG_SEPARATE_DK1, for callers short of memory) the separate dk1 pass
 // runs instead (no workspace beyond the delta / dlse rows).
 constexpr size_t kDk1PartialCap = (size_t)8 << 30;
@@ -567,7 +567,8 @@ static size_t dk1_partial_bytes(const sa_prefill_bwd_args* a) {
   const int nq = dq_queries_per_block(f.heads_q / f.heads_kv);
   const size_t qblocks = ((size_t)f.total_tokens + nq - 1) / nq;
   const size_t heads = (size_t)f.heads_q / (4 / nq);  // hk * head sub-groups
-  const size_t bytes = (qblocks * heads * (31 + nq) * f.head_dim * sizeof(float) + 255) & ~(size_t)255;
+  const size_t nr = ((size_t)f.short_window + 31) / 32;  // row groups of short keys
+  const size_t bytes = (qblocks * heads * nr * (31 + nq) * f.head_dim * sizeof(float) + 255) & ~(size_t)255;
   return bytes <= kDk1PartialCap ? bytes : 0;
 }
 // Short windows past what one MFMA dk2 / dv2 launch holds (64 keys at widths

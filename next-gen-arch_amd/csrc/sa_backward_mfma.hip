@@ -11,11 +11,11 @@
 //     dS   = bf16(P (dP - delta_t) scale)
 //     dA^T += K2^T · dS^T                        (d x j; transposing K reads)
 //     dq_t = Σ_j dA_j ⊙ k1_j
-//     with one 32-row group of short keys, also dk1: the NQ queries x NH
-//     heads of a workgroup write a partial Σ dA_{t,j} ⊙ q_{t,h} for their
-//     31 + NQ short keys j, and a fixed-order sum over the partials holding
-//     each key gives dk1 (dA_{t,j} is the dk1 pass's G_{t,j}); the dk1 pass
-//     below is then not launched
+//     with one or two 32-row groups of short keys, also dk1: per row group
+//     the NQ queries x NH heads of a workgroup write a partial Σ dA_{t,j} ⊙
+//     q_{t,h} for their 31 + NQ short keys j, and a fixed-order sum over the
+//     partials holding each key gives dk1 (dA_{t,j} is the dk1 pass's
+//     G_{t,j}); the dk1 pass below is then not launched
 //   dk1/dv1 pass (one wave per (j, h); its 32 rows are the queries
 //   t = j + 32r + n whose short window holds j; tiles span the rows' union of
 //   long windows, masked per row)
@@ -255,9 +255,10 @@ struct BwdGeo {
 // dq: a workgroup of 4 waves owns NQ consecutive queries x NH heads of one KV
 // group (the forward kernel's blocking); chunk c of the NQ queries' long
 // windows is one K2/V2 tile of 32 + NQ - 1 rows.
-// FUSE (one row group): the pass also writes the block's dk1 partial, Σ over
-// its NQ queries and NH heads of dA_{t,j} ⊙ q_{t,h} for the short keys
-// j = t0 - 31 .. t0 + NQ - 1 (the dk1 pass's G_{t,j} is the same dA_{t,j}).
+// FUSE (one or two row groups): the pass also writes the block's dk1
+// partials, per row group r Σ over its NQ queries and NH heads of dA_{t,j} ⊙
+// q_{t,h} for the short keys j = t0 - 32 r - 31 .. t0 - 32 r + NQ - 1 (the dk1
+// pass's G_{t,j} is the same dA_{t,j}).
 // F32: fp32 inputs (DK == DV <= 128): K2 / V2 tiles from the hi/lo rows
 // (p.k2s, p.v2s), the short slot and the q / dout rows hold fp32 rows (the
 // same bytes as a hi/lo row), A and B are split from fp32 products, and every
@@ -522,7 +523,7 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_d
       constexpr int ROWS1 = 31 + NQ;            // partial rows
       const char* qrow = qslot + wid * G::RSK;  // q row of this wave's (t, h)
       float* part = (float*)lds;                // [NW][32][PRS] (ring region)
-      float* const dst = p.dk1p + ((int64_t)hg * geo.qblocks + qb) * (ROWS1 * DK);
+      float* const dst = p.dk1p + (((int64_t)hg * geo.qblocks + qb) * geo.nr + r) * (ROWS1 * DK);
 #pragma unroll
       for (int dh = 0; dh < DK / 64; ++dh) {
         float* pw = part + (wid * 32 + (fresh_lane() & 31)) * PRS;
@@ -951,13 +952,14 @@ hipError_t launch_dkv1_d(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
   return launch_dkv1_t<DK, DV, 4, 1, F32>(p, geo, stream);
 }
 
-// dk1[j, g] = Σ_{head sub-groups hs of g} Σ_{query blocks qb}
-// partial[g*hsub + hs][qb][j - nq qb + 31], over the blocks whose rows hold j
-// (nq qb in [j - nq + 1, j + 31]), sub-groups then blocks in ascending order.
-// nq = queries per dq workgroup, hsub = head sub-groups per KV group.  One
-// thread per (j, g, 4 values of d).
+// dk1[j, g] = Σ_{head sub-groups hs of g} Σ_{row groups r} Σ_{query blocks qb}
+// partial[g*hsub + hs][qb][r][j - nq qb + 31 + 32 r], over the blocks whose
+// group-r rows hold j (nq qb in [j + 32 r - nq + 1, j + 32 r + 31]), in that
+// nesting and ascending order.  nq = queries per dq workgroup, hsub = head
+// sub-groups per KV group, nr = row groups.  One thread per (j, g, 4 values
+// of d).
 template <int D>
-__global__ __launch_bounds__(256) void bwd_dk1_sum_kernel(BwdParams p, int qblocks, int nq, int hsub) {
+__global__ __launch_bounds__(256) void bwd_dk1_sum_kernel(BwdParams p, int qblocks, int nq, int hsub, int nr) {
   constexpr int D4 = D / 4;
   const int64_t i = (int64_t)bid_x() * 256 + tid_x();
   const int64_t jg = i / D4;
@@ -965,13 +967,15 @@ __global__ __launch_bounds__(256) void bwd_dk1_sum_kernel(BwdParams p, int qbloc
   const int d4 = (int)(i % D4);
   const int g = (int)(jg % p.hk), j = (int)(jg / p.hk);
   const int rows = 31 + nq;
-  const int qlo = j / nq, qhi = min((j + 31) / nq, qblocks - 1);
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int hs = 0; hs < hsub; ++hs) {
-    const float* base = p.dk1p + (int64_t)(g * hsub + hs) * qblocks * rows * D + 4 * d4;
-    for (int qb = qlo; qb <= qhi; ++qb) {
-      const floatx4 x = *(const floatx4*)(base + ((int64_t)qb * rows + (j - nq * qb + 31)) * D);
-      acc += x;
+    const float* base = p.dk1p + (int64_t)(g * hsub + hs) * qblocks * nr * rows * D + 4 * d4;
+    for (int r = 0; r < nr; ++r) {
+      const int qlo = (j + 32 * r) / nq, qhi = min((j + 32 * r + 31) / nq, qblocks - 1);
+      for (int qb = qlo; qb <= qhi; ++qb) {
+        const floatx4 x = *(const floatx4*)(base + (((int64_t)qb * nr + r) * rows + (j - nq * qb + 31 + 32 * r)) * D);
+        acc += x;
+      }
     }
   }
   const int64_t off = (int64_t)j * p.dk_st + (int64_t)g * p.dk_sh + 4 * d4;
@@ -1658,17 +1662,18 @@ hipError_t launch_bwd_dkv1_mfma(const BwdParams& p, hipStream_t stream) {
   return by_widths<true>(p, [&](auto dk, auto dv) { return launch_dkv1_d<decltype(dk)::value, decltype(dv)::value>(p, geo, stream); });
 }
 bool bwd_dk1_fused_ok(const BwdParams& p) {
-  return bwd_mfma_ok(p) && p.ws <= 32 && p.dk_st % 4 == 0 && p.dk_sh % 4 == 0 && ((uintptr_t)p.dk1 & 7) == 0;
+  return bwd_mfma_ok(p) && p.ws <= (p.f32 ? 32 : 64);
 }
 
 hipError_t launch_bwd_dk1_sum(const BwdParams& p, hipStream_t stream) {
   const int nq = dq_queries_per_block(p.group), hsub = p.group / (4 / nq);
   const int qblocks = (p.tokens + nq - 1) / nq;
+  const int nr = (p.ws + 31) / 32;
   const int64_t threads = (int64_t)p.tokens * p.hk * (p.d / 4);
   const dim3 grid((unsigned)((threads + 255) / 256));
-  if (p.d == 64) hipLaunchKernelGGL(bwd_dk1_sum_kernel<64>, grid, dim3(256), 0, stream, p, qblocks, nq, hsub);
-  else if (p.d == 128) hipLaunchKernelGGL(bwd_dk1_sum_kernel<128>, grid, dim3(256), 0, stream, p, qblocks, nq, hsub);
-  else hipLaunchKernelGGL(bwd_dk1_sum_kernel<256>, grid, dim3(256), 0, stream, p, qblocks, nq, hsub);
+  if (p.d == 64) hipLaunchKernelGGL(bwd_dk1_sum_kernel<64>, grid, dim3(256), 0, stream, p, qblocks, nq, hsub, nr);
+  else if (p.d == 128) hipLaunchKernelGGL(bwd_dk1_sum_kernel<128>, grid, dim3(256), 0, stream, p, qblocks, nq, hsub, nr);
+  else hipLaunchKernelGGL(bwd_dk1_sum_kernel<256>, grid, dim3(256), 0, stream, p, qblocks, nq, hsub, nr);
   return hipGetLastError();
 }
 

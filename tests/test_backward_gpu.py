@@ -163,19 +163,21 @@ def test_backward_mfma_matches_portable(cuda):
         assert err <= bound, name
 
 
-# ---- dk1 from the dq pass (bf16, D == DV in {64, 128}, short window <= 32):
-# each dq workgroup writes a partial of Σ dA_{t,j} ⊙ q_{t,h} over its queries
-# and heads that a fixed-order sum turns into dk1 ----------------------------------
+# ---- dk1 from the dq pass (bf16, short window <= 64): each dq workgroup
+# writes, per 32-row group of short keys, a partial of Σ dA_{t,j} ⊙ q_{t,h}
+# over its queries and heads that a fixed-order sum turns into dk1 ---------------
 
 @pytest.mark.parametrize("b,n,hq,hk,d,ws,wl", [(1, 200, 4, 4, 128, 32, 96), (2, 37, 3, 3, 64, 20, 70),
                                                (1, 150, 6, 2, 128, 32, 200), (2, 61, 2, 2, 128, 5, 40),
                                                (1, 90, 3, 1, 64, 1, 1), (2, 77, 4, 2, 64, 32, 70),
-                                               (1, 50, 8, 2, 128, 32, 100)])
+                                               (1, 50, 8, 2, 128, 32, 100),
+                                               (2, 75, 3, 1, 128, 64, 90), (1, 130, 6, 3, 64, 48, 70),
+                                               (1, 99, 8, 2, 128, 33, 120)])
 def test_backward_bf16_dk1_from_dq(cuda, b, n, hq, hk, d, ws, wl):
     """MHA, GQA groups of 3 (4 queries x 1 head per dq workgroup), 2 (2 x 2)
-    and 4 (1 x 4) with a full 32-row short window, token counts not a
-    multiple of 4 (a partial last query block), batch boundaries inside a
-    block, and single pairs."""
+    and 4 (1 x 4) with one or two 32-row groups of short keys, token counts
+    not a multiple of 4 (a partial last query block), batch boundaries inside
+    a block, and single pairs."""
     _run(cuda, b, n, hq, hk, d, ws, wl, torch.bfloat16, seed=n + ws)
 
 
@@ -246,11 +248,12 @@ def test_backward_bf16_separate_dk1_when_partials_do_not_fit(cuda, monkeypatch):
     monkeypatch.setattr(shim.torch, "empty", empty)
     _run(cuda, 1, 200, 4, 4, 128, 32, 96, torch.bfloat16, seed=77)
     _run(cuda, 2, 61, 6, 2, 64, 20, 70, torch.bfloat16, seed=78)
+    _run(cuda, 1, 200, 4, 4, 128, 64, 96, torch.bfloat16, seed=80)  # two row groups of short keys
     # fp32: the dk1 pass on the matrix cores (shape chosen so that the forward's
     # fp32 workspace stays under the refused size)
     _run(cuda, 1, 200, 4, 2, 128, 32, 96, torch.float32, seed=79)
     monkeypatch.undo()
-    assert len(refused) == 3, refused  # one refused partials workspace per call, then the small one
+    assert len(refused) == 4, refused  # one refused partials workspace per call, then the small one
 
 
 # ---- fp32 inputs on the matrix cores: every operand as hi + lo bf16 terms,
@@ -370,7 +373,7 @@ def test_backward_bf16_two_short_row_groups_match_portable(cuda):
 @pytest.mark.parametrize("b,n,hq,hk,d,dv,ws,wl", [
     (1, 150, 4, 4, 128, 64, 32, 96),  # MHA, dk1 from the dq pass
     (2, 61, 6, 3, 128, 64, 20, 70),   # GQA 2
-    (1, 90, 8, 2, 128, 64, 64, 100),  # GQA 4, two short row groups (separate dk1 pass)
+    (1, 90, 8, 2, 128, 64, 64, 100),  # GQA 4, two short row groups (dk1 partials per row group)
     (1, 77, 3, 1, 64, 128, 32, 50),   # DV > DK, GQA 3
     (2, 40, 4, 2, 64, 128, 45, 60),   # DV > DK, two short row groups
     (1, 50, 2, 2, 128, 64, 1, 1),     # single pairs
@@ -424,7 +427,7 @@ def test_backward_bf16_value_width_differs_matches_portable_and_repeats(cuda, d,
     (1, 90, 4, 2, 256, 256, 32, 96),   # GQA 2, dk1 from the dq pass
     (2, 37, 3, 3, 256, 256, 20, 40),   # MHA (4 queries per dq workgroup), partial last block
     (1, 70, 8, 2, 256, 128, 32, 64),   # GQA 4, DV 128
-    (1, 60, 4, 4, 256, 256, 40, 60),   # two short row groups: the separate dk1 pass, dk2 / dv2 in two launches
+    (1, 60, 4, 4, 256, 256, 40, 60),   # two short row groups: dk1 from the dq pass, dk2 / dv2 in two launches
     (1, 80, 4, 2, 256, 128, 64, 100),  # a full 64-key short window, GQA 2, DV 128
     (1, 50, 2, 2, 256, 256, 70, 80),   # short window past 64: portable dk2 / dv2
     (1, 33, 2, 2, 256, 128, 1, 1),     # single pairs
@@ -494,3 +497,48 @@ def test_backward_bf16_short_windows_past_64_varlen_matches_portable_and_repeats
         bound = 2e-2 * max(b.abs().max().item(), 1.0)
         print(f"ws 110 mfma vs portable {name}: {err:.2e} / {bound:.1e}", flush=True)
         assert err <= bound, name
+
+
+def test_backward_c4_full_size_dk1_partials_match_separate_pass(cuda, monkeypatch):
+    """C4 at its full size (S 16384, H 8, D 256, windows 256 x 64: two 32-row
+    groups of short keys): dk1 from the dq pass's per-group partials agrees with
+    the separate dk1 pass to bf16 precision, the other gradients come from the
+    same kernels either way (bitwise equal), and a second call is bitwise
+    identical."""
+    import archlab_amd.architectures.simplicial_attention as shim
+    from archlab_amd import simplicial_attention
+    from archlab_amd import workloads as W
+    cfg = W.C4
+    q, k1, k2, v1, v2, _ = W.prefill_inputs(cfg, device=cuda)
+    dout = torch.randn(q.shape[:-1] + (v1.shape[-1],), device=cuda).to(cfg.dtype)
+
+    def grads():
+        xd = [t.detach().clone().requires_grad_(True) for t in (q, k1, k2, v1, v2)]
+        out = simplicial_attention(*xd, cfg.w2, cfg.w1, scale=1.0)  # q carries 1/sqrt(D)
+        out.backward(dout)
+        return [t.grad for t in xd]
+
+    fused = grads()
+    again = grads()
+    for name, a, b in zip(("dq", "dk1", "dk2", "dv1", "dv2"), fused, again):
+        assert torch.equal(a, b), name
+    real_empty = torch.empty
+
+    def empty(*size, **kw):  # refuse the workspace that holds the dk1 partials (2.3 GB at C4)
+        n = size[0] if size and isinstance(size[0], int) else None
+        if kw.get("dtype") is torch.uint8 and n is not None and n > (1 << 30):
+            raise torch.cuda.OutOfMemoryError("workspace refused by the test")
+        return real_empty(*size, **kw)
+
+    monkeypatch.setattr(shim.torch, "empty", empty)
+    separate = grads()
+    monkeypatch.undo()
+    for name, a, b in zip(("dq", "dk1", "dk2", "dv1", "dv2"), fused, separate):
+        a, b = a.float(), b.float()
+        err = (a - b).abs().max().item()
+        bound = 1e-2 * max(b.abs().max().item(), 1.0)
+        print(f"C4 fused vs separate dk1 {name}: {err:.2e} / {bound:.1e}", flush=True)
+        if name in ("dk2", "dv1", "dv2"):
+            assert torch.equal(a, b), name
+        else:
+            assert err <= bound, name

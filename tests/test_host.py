@@ -334,18 +334,19 @@ def test_paged_accepts_the_reference_mixed_index_dtypes_before_launch():
 @pytest.mark.parametrize("dtype,hq,hk,d,dv,ws,fused", [
     ("bf16", 4, 4, 128, 128, 32, True), ("bf16", 6, 2, 64, 64, 20, True), ("bf16", 8, 2, 128, 128, 32, True),
     ("bf16", 4, 2, 64, 64, 32, True), ("bf16", 4, 4, 128, 64, 32, True), ("bf16", 6, 2, 64, 128, 8, True),
-    ("bf16", 4, 4, 128, 128, 40, False), ("f32", 4, 4, 64, 64, 32, True), ("f32", 6, 2, 128, 128, 20, True), ("bf16", 4, 4, 256, 128, 32, True),
-    ("bf16", 8, 2, 256, 256, 16, True), ("bf16", 4, 4, 256, 64, 32, False), ("bf16", 4, 4, 256, 256, 40, False),
-    ("bf16", 4, 2, 256, 128, 64, False), ("bf16", 4, 4, 256, 256, 65, False), ("bf16", 4, 2, 128, 64, 100, False),
-    ("bf16", 4, 4, 64, 64, 128, False), ("bf16", 4, 4, 64, 64, 129, False), ("f32", 4, 4, 128, 128, 100, False)])
+    ("bf16", 4, 4, 128, 128, 40, True), ("f32", 4, 4, 64, 64, 32, True), ("f32", 6, 2, 128, 128, 20, True), ("bf16", 4, 4, 256, 128, 32, True),
+    ("bf16", 8, 2, 256, 256, 16, True), ("bf16", 4, 4, 256, 64, 32, False), ("bf16", 4, 4, 256, 256, 40, True),
+    ("bf16", 4, 2, 256, 128, 64, True), ("bf16", 4, 4, 256, 256, 65, False), ("bf16", 4, 2, 128, 64, 100, False),
+    ("bf16", 4, 4, 64, 64, 128, False), ("bf16", 4, 4, 64, 64, 129, False), ("f32", 4, 4, 128, 128, 100, False),
+    ("f32", 4, 4, 128, 128, 40, False), ("bf16", 3, 1, 64, 128, 64, True)])
 def test_backward_workspace_reserves_dk1_partials_for_fused_shapes(dtype, hq, hk, d, dv, ws, fused):
     """The backward workspace holds delta and dlse rows ([tokens, hq] fp32 each,
     256-byte rounded) and, where dk1 comes from the dq pass (bf16, score width
-    D and value width each 64 or 128, or D = 256 over values of 128 or 256;
-    short window <= 32; fp32 with equal widths of 64 or 128 as well), the partials:
-    31 + NQ fp32 rows of D per
-    dq workgroup of NQ queries x 4 / NQ heads (NQ = 4, 2, 1 for GQA groups
-    that are odd, even, multiples of 4)."""
+    D and value width each 64 or 128, or D = 256 over values of 128 or 256,
+    short window <= 64; fp32 with equal widths of 64 or 128, short window
+    <= 32), the partials: 31 + NQ fp32 rows of D per dq workgroup of NQ
+    queries x 4 / NQ heads (NQ = 4, 2, 1 for GQA groups that are odd, even,
+    multiples of 4) and per 32-row group of short keys."""
     from archlab_amd import _native
     lib = _native.load()
     tokens = 1001
@@ -359,9 +360,10 @@ def test_backward_workspace_reserves_dk1_partials_for_fused_shapes(dtype, hq, hk
     args = _native.PrefillBwdArgs(fwd=fwd)
     group = hq // hk
     nq = 1 if group % 4 == 0 else 2 if group % 2 == 0 else 4
-    per_query = hq // (4 // nq) * (31 + nq) * d * 4 / nq  # partial bytes per query
+    nr = -(-ws // 32)
+    per_query = hq // (4 // nq) * nr * (31 + nq) * d * 4 / nq  # partial bytes per query
     rows = (tokens * hq * 4 + 255) // 256 * 256
-    part = (-(-tokens // nq) * (hq // (4 // nq)) * (31 + nq) * d * 4 + 255) // 256 * 256 if fused else 0
+    part = (-(-tokens // nq) * (hq // (4 // nq)) * nr * (31 + nq) * d * 4 + 255) // 256 * 256 if fused else 0
     # short windows of 65-128 at widths <= 128 (33-64 at score width 256): the
     # fp32 dk2 / dv2 sums of the first of two launches
     one = 32 if d == 256 else 64
@@ -380,8 +382,9 @@ def test_backward_workspace_reserves_dk1_partials_for_fused_shapes(dtype, hq, hk
         args.fwd.total_tokens = args.fwd.seqlen = big
         rows = (big * hq * 4 + 255) // 256 * 256
         split = 2 * ((big * hk * d * 4 + 255) // 256 * 256) if f32_mfma else 0
+        dkv2_big = (big * hk * (d + dv) * 4 + 255) // 256 * 256 if phased else 0
         walk = _walk_split_bytes(dtype, big, hk, d, dv, ws, 512)
-        assert lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args)) == 2 * rows + split + walk
+        assert lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args)) == 2 * rows + dkv2_big + split + walk
     # a caller short of memory selects the separate dk1 pass: no partials reserved
     args.fwd.total_tokens = args.fwd.seqlen = tokens
     args.fwd.flags = _native.SA_FLAG_SEPARATE_DK1
