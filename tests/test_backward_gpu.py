@@ -542,3 +542,35 @@ def test_backward_c4_full_size_dk1_partials_match_separate_pass(cuda, monkeypatc
             assert torch.equal(a, b), name
         else:
             assert err <= bound, name
+
+
+@pytest.mark.parametrize("name", ["NS", "DSV41-bf16", "DSV41"])
+def test_backward_full_size_matches_portable(cuda, name):
+    """Full-size workloads, the matrix-core backward against the portable
+    fp32-arithmetic kernels on the same inputs: NS (8-wave dk2 / dv2
+    workgroups, dk1 from the dq pass), the reference DeepSeek-V4.1 adapter
+    geometry (HQ 8 / HKV 2, windows 32 / 512, 2 x 8192 tokens) in bf16 (4-wave
+    dk2 / dv2 workgroups whose walks over the queries are split into pieces)
+    and in fp32 (hi/lo bf16 terms).  bf16 to 2e-2 x max|grad| (both paths round
+    the same operands to bf16 and differ in fp32 summation order), fp32 to
+    1e-4 x max|grad|."""
+    import dataclasses
+    from archlab_amd import simplicial_attention
+    from archlab_amd import workloads as W
+    cfg = {"NS": W.NS, "DSV41-bf16": dataclasses.replace(W.DSV41, dtype=torch.bfloat16), "DSV41": W.DSV41}[name]
+    q, k1, k2, v1, v2, _ = W.prefill_inputs(cfg, device=cuda)
+    g = torch.Generator().manual_seed(5)
+    dout = torch.randn(q.shape[:-1] + (v1.shape[-1],), generator=g).to(cfg.dtype).to(cuda)
+    grads = {}
+    for kernel in ("auto", "generic"):
+        xd = [t.detach().clone().requires_grad_(True) for t in (q, k1, k2, v1, v2)]
+        simplicial_attention(*xd, cfg.w2, cfg.w1, scale=1.0, kernel=kernel).backward(dout)  # q carries 1/sqrt(D)
+        grads[kernel] = [t.grad.float() for t in xd]
+        del xd
+    rtol = 1e-4 if cfg.dtype == torch.float32 else 2e-2
+    for gname, a, b in zip(("dq", "dk1", "dk2", "dv1", "dv2"), grads["auto"], grads["generic"]):
+        assert torch.isfinite(a).all(), gname
+        err = (a - b).abs().max().item()
+        bound = rtol * max(b.abs().max().item(), 1.0)
+        print(f"{name} full size: mfma vs portable {gname}: {err:.2e} / {bound:.1e}", flush=True)
+        assert err <= bound, gname
