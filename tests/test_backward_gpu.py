@@ -324,6 +324,40 @@ def test_backward_bf16_dk2_workgroup_widths_match_portable(cuda, hk):
         assert err <= bound, name
 
 
+# ---- dk2 / dv2 walk pieces: with few (key block, KV head) workgroups each
+# walk over the queries is cut into up to 8 pieces whose fp32 sums are added
+# in a fixed order; a last key block shorter than the piece count leaves some
+# pieces empty (they write zero sums) ------------------------------------------
+
+@pytest.mark.parametrize("b,n,hq,hk,d,ws,wl", [(1, 129, 2, 2, 128, 32, 512), (1, 130, 4, 2, 64, 20, 300),
+                                               (2, 129, 2, 1, 128, 64, 400), (1, 700, 8, 1, 128, 32, 512)])
+def test_backward_bf16_dk2_walk_pieces(cuda, b, n, hq, hk, d, ws, wl):
+    _run(cuda, b, n, hq, hk, d, ws, wl, torch.bfloat16, seed=n + wl)
+
+
+def test_backward_bf16_dk2_walk_pieces_varlen_repeatable(cuda):
+    """Packed sequences across walk pieces, against the oracle, and bitwise repeatable."""
+    from archlab_amd import simplicial_varlen_attention
+    lengths = [1, 300, 7, 180, 2]
+    t = sum(lengths)
+    x = [v[0] for v in rand_inputs(1, t, 4, 1, 128, seed=41, dtype=torch.bfloat16)]
+    g = torch.Generator().manual_seed(12)
+    dout = torch.randn(t, 4, 128, generator=g).bfloat16()
+    cu = torch.tensor([0, 1, 301, 308, 488, 490], dtype=torch.int32)
+    runs = []
+    for _ in range(2):
+        xd = [v.to(cuda).requires_grad_(True) for v in x]
+        out = simplicial_varlen_attention(*xd, cu.to(cuda), 32, 400)
+        (out.float() * dout.to(cuda).float()).sum().backward()
+        runs.append([v.grad for v in xd])
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+    xs = [v.double().requires_grad_(True) for v in x]
+    o = O.varlen_reference(*xs, cu, 32, 400, scale=128 ** -0.5)
+    (o * dout.double()).sum().backward()
+    _assert_grads(runs[0], [v.grad.float() for v in xs], torch.bfloat16, "varlen bf16 walk pieces")
+
+
 # ---- dk2 / dv2 on the matrix cores with short windows of 33-64 (two 32-row
 # groups of short keys per step) ----------------------------------------------------
 
