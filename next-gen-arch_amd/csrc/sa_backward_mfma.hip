@@ -38,10 +38,13 @@ namespace sa {
 
 namespace {
 
-// LDS fragments read ahead of their MFMA in each pass (see BwdOps)
-constexpr int kDqPF = 1;    // dq pass
-constexpr int kDk1PF = 1;   // dk1 / dv1 pass (dv1 reads two ahead)
-constexpr int kDkv2PF = 2;  // dk2 / dv2 pass
+// LDS fragments read ahead of their MFMA in each pass (see BwdOps); at score
+// width 256 (one wave per SIMD: no other wave hides the LDS latency) the dq
+// and dk2 / dv2 passes read further ahead (C4 forward + backward 29.1 ->
+// 28.7 and 28.9 ms)
+constexpr int kDqPF = 1, kDqPFWide = 3;      // dq pass
+constexpr int kDk1PF = 1;                    // dk1 / dv1 pass (dv1 reads two ahead)
+constexpr int kDkv2PF = 2, kDkv2PFWide = 4;  // dk2 / dv2 pass
 
 constexpr size_t kLdsPerCu = 160 * 1024;  // gfx950
 constexpr int kMaxWalkSplits = 8;         // dk2 / dv2 walk pieces per (key block, KV head)
@@ -276,6 +279,7 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_d
   using OPV = BwdOps<DV>;  // ... over the value width
   constexpr int R = P + 1;
   constexpr int NI = G::NI;
+  constexpr int kPF = DK >= 256 ? kDqPFWide : kDqPF;
   // ring of R tile slots, also the per-wave reduction scratch of the epilogue
   constexpr int RING = R * G::SLOT > NW * 64 * 36 * 4 ? R * G::SLOT : NW * 64 * 36 * 4;
   extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -435,8 +439,8 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_d
         s = OPK::template rows_x_hl<G::RSK>(slot, qo, lane, ra.a, ra.al);
         dp = OPV::template rows_x_hl<G::RSV>(slot + G::VOFF, qo, lane, rbv.a, rbv.al);
       } else {
-        s = OPK::template rows_x<G::RSK, kDqPF>(slot, qo, lane, ra.a);
-        dp = OPV::template rows_x<G::RSV, kDqPF>(slot + G::VOFF, qo, lane, rbv.a);
+        s = OPK::template rows_x<G::RSK, kPF>(slot, qo, lane, ra.a);
+        dp = OPV::template rows_x<G::RSV, kPF>(slot + G::VOFF, qo, lane, rbv.a);
       }
       // register r holds chunk key 8*(r/4) + r%4 + 4*half of column j = this lane's row
       const int lo_h = klo - 4 * half, hi_h = khi - 4 * half;
@@ -461,7 +465,7 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_d
         OPK::template tr_acc_hl<G::RSK>(dA, slot, qo, lane, pb0, pb1, pl0, pl1);  // dA^T += K2^T · dS^T
       } else {
         OPK::pack_c(ds, pb0, pb1);
-        OPK::template tr_acc<G::RSK, kDqPF>(dA, slot, qo, lane, pb0, pb1);  // dA^T += K2^T · dS^T
+        OPK::template tr_acc<G::RSK, kPF>(dA, slot, qo, lane, pb0, pb1);  // dA^T += K2^T · dS^T
       }
     }
     wait_vmcnt<0>();
@@ -1032,7 +1036,7 @@ __global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_
   constexpr int RPW = 32 / NWK;   // A / B rows formed per wave and step
   // LDS reads in flight ahead of their MFMA: with two waves per SIMD, one
   // read ahead leaves each step's three MFMA chains waiting on LDS latency
-  constexpr int kPF = kDkv2PF;
+  constexpr int kPF = DK >= 256 ? kDkv2PFWide : kDkv2PF;
   static_assert(kDK || kDV, "one output per launch");
   constexpr int XW = kDK ? DK : DV;        // width of the gradient accumulated
   using OPK = BwdOps<DK>;

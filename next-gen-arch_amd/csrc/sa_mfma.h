@@ -467,9 +467,10 @@ struct RowBlock {
     floatx16 s = floatx16{};
     {
       // K fragments are read two steps ahead of their MFMA (one ahead measured
-      // 0.5-0.9 % slower at widths of 128); the scheduling barriers stop the
-      // compiler from hoisting all DK/16 reads (which would hold DK/4 extra
-      // VGPRs live).
+      // 0.5-0.9 % slower at widths of 128; four at score width 512, one wave
+      // per SIMD with accumulation registers to spare: DS 512 6.20 -> 6.14
+      // ms); the scheduling barriers stop the compiler from hoisting all DK/16
+      // reads (which would hold DK/4 extra VGPRs live).
       const char* kp = ktile + (row0 + n) * RSK + 16 * half;
       if constexpr (KL) {
 #pragma unroll
@@ -483,11 +484,12 @@ struct RowBlock {
         }
       } else {
         bf16x8 kq[DK / 16];
-        kq[0] = *(const bf16x8*)kp;
-        if (DK / 16 > 1) kq[1] = *(const bf16x8*)(kp + 32);
+        constexpr int KA = DK >= 512 ? 4 : 2;  // fragments read ahead
+#pragma unroll
+        for (int t = 0; t < KA && t < DK / 16; ++t) kq[t] = *(const bf16x8*)(kp + 32 * t);
 #pragma unroll
         for (int t = 0; t < DK / 16; ++t) {
-          if (t + 2 < DK / 16) kq[t + 2] = *(const bf16x8*)(kp + 32 * (t + 2));
+          if (t + KA < DK / 16) kq[t + KA] = *(const bf16x8*)(kp + 32 * (t + KA));
           __builtin_amdgcn_sched_barrier(0);
           s = qk_mfma(kq[t], t, s);
           __builtin_amdgcn_sched_barrier(0);

@@ -66,9 +66,8 @@ struct PrefillParams {
 
 constexpr int kPrefillWavesPerSimd = 3;  // widths <= 128, bf16
 // V fragments read ahead of the PV MFMAs in the chunk loop (2 measured
-// 0.1-0.9 % ahead of 3 and 4); reading K fragments further ahead than one
-// spills in the loop
-constexpr int kPrefillChunkPF = 2;
+// 0.1-0.9 % ahead of 3 and 4; at score width 512, one wave per SIMD, 4)
+constexpr int kPrefillChunkPF = 2, kPrefillChunkPFWide = 4;
 
 // One wave per (token, head), NQ x NH = 4 of them per workgroup; one K/V
 // tile in flight (a two-slot ring).
@@ -315,7 +314,7 @@ void prefill_mfma_kernel(PrefillParams p) {
         const bool active = qvalid && c >= cfirst;
         const int kfirst = t - p.wl + 1 + kChunk * c;  // key of this wave's chunk row 0
         const char* slot = slot_of(c);
-        rb.template chunk<G::RSK, G::RSV, kPrefillChunkPF>(slot, slot + G::VOFF, qo, lane, p.sl2,
+        rb.template chunk<G::RSK, G::RSV, (DK >= 512 ? kPrefillChunkPFWide : kPrefillChunkPF)>(slot, slot + G::VOFF, qo, lane, p.sl2,
                                                                active ? max(lo2 - kfirst, 0) : kChunk,
                                                                active ? min(t - kfirst, kChunk - 1) : -1);
       }
