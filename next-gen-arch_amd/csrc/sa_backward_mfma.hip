@@ -95,10 +95,17 @@ struct BwdOps {
   // transposed (d x rows, read with ds_read_b64_tr_b16), B operand = {pb0,
   // pb1}: the 32 x 32 values of a rows_x result (rows x columns) packed by
   // pack_c.  acc[db] holds d = 32*db + acc_row(r, half), column lane % 32.
+  // OT: the same product with the operands swapped, (PB^T · Tile): acc[db]
+  // holds column d = 32*db + lane % 32 and, in register r, the rows_x column
+  // (x row) 8*(r/4) + 4*half + r%4.
   // PF: transposed reads issued that many MFMAs ahead.
-  template <int RS, int PF = 1>
+  template <int RS, int PF = 1, bool OT = false>
   __device__ static __forceinline__ void tr_acc(floatx16* acc, const char* tile, int row0, int lane,
                                                 const bf16x8& pb0, const bf16x8& pb1) {
+    auto mm = [](const bf16x8& v, const bf16x8& b, const floatx16& c) {
+      if constexpr (OT) return mfma32x32x16(b, v, c);
+      else return mfma32x32x16(v, b, c);
+    };
     const int half = lane >> 5, g16 = (lane >> 4) & 1, i16 = lane & 15;
     const int e_src = i16 >> 2, q_src = i16 & 3;
     const uint32_t vp = lds_addr(tile + (row0 + 4 * half + e_src) * RS + 32 * g16 + 8 * q_src);
@@ -115,7 +122,7 @@ struct BwdOps {
         shortx8 vv = {va[s][0], va[s][1], va[s][2], va[s][3], vb[s][0], vb[s][1], vb[s][2], vb[s][3]};
         const bf16x8 vf = __builtin_bit_cast(bf16x8, vv);
         __builtin_amdgcn_sched_barrier(0);
-        acc[s % (D / 32)] = mfma32x32x16(vf, s / (D / 32) == 0 ? pb0 : pb1, acc[s % (D / 32)]);
+        acc[s % (D / 32)] = mm(vf, s / (D / 32) == 0 ? pb0 : pb1, acc[s % (D / 32)]);
         __builtin_amdgcn_sched_barrier(0);
       });
       return;
@@ -130,7 +137,7 @@ struct BwdOps {
       shortx4 n1, n2;
       if constexpr (step + 1 < kSteps) RB::template vread<RS, step + 1>(vp, n1, n2);
       __builtin_amdgcn_sched_barrier(0);
-      acc[step % (D / 32)] = mfma32x32x16(vf, step / (D / 32) == 0 ? pb0 : pb1, acc[step % (D / 32)]);
+      acc[step % (D / 32)] = mm(vf, step / (D / 32) == 0 ? pb0 : pb1, acc[step % (D / 32)]);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (step + 1 < kSteps) {
         lds_wait(n1, n2);
@@ -280,6 +287,12 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_d
   constexpr int R = P + 1;
   constexpr int NI = G::NI;
   constexpr int kPF = DK >= 256 ? kDqPFWide : kDqPF;
+  // dA with the lane on d (the MFMA operands swapped) at score width 256: the
+  // epilogue sums the rows in registers instead of through a per-wave LDS
+  // transpose of 128 values per lane (C4 forward + backward 28.35 -> 27.6 ms);
+  // at widths up to 128 the row layout's 16-byte staging writes of the dk1
+  // partials measured ahead (adapter shape 8.8 against 9.0 ms)
+  constexpr bool kOT = !F32 && DK >= 256;
   // ring of R tile slots, also the per-wave reduction scratch of the epilogue
   constexpr int RING = R * G::SLOT > NW * 64 * 36 * 4 ? R * G::SLOT : NW * 64 * 36 * 4;
   extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -465,64 +478,108 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_d
         OPK::template tr_acc_hl<G::RSK>(dA, slot, qo, lane, pb0, pb1, pl0, pl1);  // dA^T += K2^T · dS^T
       } else {
         OPK::pack_c(ds, pb0, pb1);
-        OPK::template tr_acc<G::RSK, kPF>(dA, slot, qo, lane, pb0, pb1);  // dA^T += K2^T · dS^T
+        OPK::template tr_acc<G::RSK, kPF, kOT>(dA, slot, qo, lane, pb0, pb1);  // dA^T += K2^T · dS^T (kOT: dA, lane = d)
       }
     }
     wait_vmcnt<0>();
     block_barrier();  // ring reads done (LDS reused below)
 
-    // dq[d] += Σ_j dA_j[d] k1_j[d] over the wave's 32 rows
-    float* red = (float*)lds + wid * (64 * 36);  // [64 d][36] per wave (ring region)
-    const char* k1s = sslot + srow * G::RSK;     // this lane's k1 row
-    floatx4 kv[DK / 64][2][4];
+    // rows n of the wave inside the short window: n < nv (j = t - 32 r - n >= lo1)
+    const int nv = qvalid ? min(32, t - 32 * r - lo1 + 1) : 0;
+    if constexpr (!kOT) {
+      // dq[d] += Σ_j dA_j[d] k1_j[d] over the wave's 32 rows (dA^T: lane = row)
+      float* red = (float*)lds + wid * (64 * 36);  // [64 d][36] per wave (ring region)
+      const char* k1s = sslot + srow * G::RSK;     // this lane's k1 row
+      floatx4 kv[DK / 64][2][4];
 #pragma unroll
-    for (int sl = 0; sl < DK / 64; ++sl)
+      for (int sl = 0; sl < DK / 64; ++sl)
 #pragma unroll
-      for (int dbl = 0; dbl < 2; ++dbl)
+        for (int dbl = 0; dbl < 2; ++dbl)
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const int dd = 64 * sl + 32 * dbl + 8 * q4 + 4 * half;
-          if constexpr (F32) {
-            kv[sl][dbl][q4] = *(const floatx4*)(k1s + 4 * dd);
-          } else {
-            const bf16x4 kb = *(const bf16x4*)(k1s + 2 * dd);
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const int dd = 64 * sl + 32 * dbl + 8 * q4 + 4 * half;
+            if constexpr (F32) {
+              kv[sl][dbl][q4] = *(const floatx4*)(k1s + 4 * dd);
+            } else {
+              const bf16x4 kb = *(const bf16x4*)(k1s + 2 * dd);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) kv[sl][dbl][q4][e] = (float)kb[e];
+              for (int e = 0; e < 4; ++e) kv[sl][dbl][q4][e] = (float)kb[e];
+            }
+          }
+#pragma unroll
+      for (int sl = 0; sl < DK / 64; ++sl) {
+#pragma unroll
+        for (int dbl = 0; dbl < 2; ++dbl) {
+          const int db = 2 * sl + dbl;
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const int dd = 32 * dbl + 8 * q4 + 4 * half;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float k = row_ok ? kv[sl][dbl][q4][e] : 0.f;
+              red[(dd + e) * 36 + n] = k * dA[db][4 * q4 + e];
+            }
           }
         }
+        // `red` is private to this wave and a wave's LDS accesses execute in order
+        float acc = 0.f;
+        const floatx4* row4 = (const floatx4*)(red + lane * 36);
 #pragma unroll
-    for (int sl = 0; sl < DK / 64; ++sl) {
-#pragma unroll
-      for (int dbl = 0; dbl < 2; ++dbl) {
-        const int db = 2 * sl + dbl;
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const int dd = 32 * dbl + 8 * q4 + 4 * half;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float k = row_ok ? kv[sl][dbl][q4][e] : 0.f;
-            red[(dd + e) * 36 + n] = k * dA[db][4 * q4 + e];
-          }
+        for (int i = 0; i < 8; ++i) {
+          floatx4 x = row4[i];
+          acc += (x[0] + x[1]) + (x[2] + x[3]);
         }
+        dqrun[sl] += acc;
       }
-      // `red` is private to this wave and a wave's LDS accesses execute in order
-      float acc = 0.f;
-      const floatx4* row4 = (const floatx4*)(red + lane * 36);
+    } else {
+      // dA (lane = d) holds column d = 32 db + lane % 32 and, in register
+      // 4 g + e, row n = 8 g + 4 half + e (short-slot row qo + 31 - n): dq[d] =
+      // Σ_n dA_n[d] k1_n[d] in registers over the 16 rows of this half, the k1
+      // values read transposed from the short slot, plus the other half's sum.
+      // Rows outside the window hold dA = 0; in a partial window they are also
+      // dropped from the sum (a k1 row outside it need not be finite).
+      const int lf = fresh_lane();
+      const int hf = lf >> 5, g16 = (lf >> 4) & 1, i16 = lf & 15;
+      const uint32_t k1p = lds_addr(sslot + (qo + 7 - 4 * hf - (i16 >> 2)) * G::RSK + 32 * g16 + 8 * (i16 & 3));
+      static_for<0, DK / 32>([&](auto dd) {
+        constexpr int db = decltype(dd)::value;
+        shortx4 x[4];
+        static_for<0, 4>([&](auto gg) {
+          constexpr int gi = decltype(gg)::value;
+          x[gi] = ds_read_tr16<(24 - 8 * gi) * G::RSK + 64 * db>(k1p);
+        });
+        lds_wait(x[0], x[1]);
+        lds_wait(x[2], x[3]);
+        float acc = 0.f;
+        if (nv >= 32) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        floatx4 x = row4[i];
-        acc += (x[0] + x[1]) + (x[2] + x[3]);
-      }
-      dqrun[sl] += acc;
+          for (int g4 = 0; g4 < 4; ++g4)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc = fmaf(bf16_bits_to_f32(x[g4][e]), dA[db][4 * g4 + e], acc);
+        } else {
+          // an opaque copy of nv keeps the row tests inside this rare branch
+          int nvm = nv;
+          asm volatile("" : "+s"(nvm));
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float k = 8 * g4 + 4 * hf + e < nvm ? bf16_bits_to_f32(x[g4][e]) : 0.f;
+              acc = fmaf(k, dA[db][4 * g4 + e], acc);
+            }
+        }
+        // both halves hold column d's sum; the half of block db's parity keeps it
+        const float tot = pair_sum(acc);
+        dqrun[db >> 1] = hf == (db & 1) ? dqrun[db >> 1] + tot : dqrun[db >> 1];
+      });
     }
-    block_barrier();  // every wave's `red` reads done before the next pass (or exit) reuses the LDS
+    block_barrier();  // every wave's short-slot (and `red`) reads done before the next pass (or exit) reuses the LDS
 
     if constexpr (FUSE) {
-      // dk1 partial: lane n of wave (qo, hw) holds row j = t0 + qo - n,
-      // partial row jrow = j - (t0 - 31) = qo + 31 - n.  Per 64-wide d half,
-      // each wave stages its 32 rows x 64 d products (rows of 68 floats, 4
-      // consecutive d per 16-byte write), then the block sums every
-      // (jrow, 4 d) over its waves in wave order and writes it.
+      // dk1 partial: row n of wave (qo, hw) is short key j = t0 + qo - 32 r - n,
+      // partial row jrow = qo + 31 - n.  Per 64-wide d half, each wave stages
+      // its 32 rows x 64 d products (rows of 68 floats), then the block sums
+      // every (jrow, 4 d) over its waves in wave order and writes it.
       constexpr int PRS = 68;                   // staged row stride (floats)
       constexpr int ROWS1 = 31 + NQ;            // partial rows
       const char* qrow = qslot + wid * G::RSK;  // q row of this wave's (t, h)
@@ -530,25 +587,55 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_d
       float* const dst = p.dk1p + (((int64_t)hg * geo.qblocks + qb) * geo.nr + r) * (ROWS1 * DK);
 #pragma unroll
       for (int dh = 0; dh < DK / 64; ++dh) {
-        float* pw = part + (wid * 32 + (fresh_lane() & 31)) * PRS;
+        if constexpr (!kOT) {
+          // dA^T: lane n holds row n, 4 consecutive d per 16-byte write
+          float* pw = part + (wid * 32 + (fresh_lane() & 31)) * PRS;
 #pragma unroll
-        for (int dbl = 0; dbl < 2; ++dbl)
+          for (int dbl = 0; dbl < 2; ++dbl)
 #pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4) {
-            const int dd = 32 * dbl + 8 * q4 + 4 * half;
-            floatx4 qv;
-            if constexpr (F32) {
-              qv = *(const floatx4*)(qrow + 4 * (64 * dh + dd));
-            } else {
-              const bf16x4 qb = *(const bf16x4*)(qrow + 2 * (64 * dh + dd));
+            for (int q4 = 0; q4 < 4; ++q4) {
+              const int dd = 32 * dbl + 8 * q4 + 4 * half;
+              floatx4 qv;
+              if constexpr (F32) {
+                qv = *(const floatx4*)(qrow + 4 * (64 * dh + dd));
+              } else {
+                const bf16x4 qb4 = *(const bf16x4*)(qrow + 2 * (64 * dh + dd));
 #pragma unroll
-              for (int e = 0; e < 4; ++e) qv[e] = (float)qb[e];
+                for (int e = 0; e < 4; ++e) qv[e] = (float)qb4[e];
+              }
+              floatx4 x;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) x[e] = row_ok ? qv[e] * dA[2 * dh + dbl][4 * q4 + e] : 0.f;
+              *(floatx4*)(pw + dd) = x;
             }
-            floatx4 x;
+        } else {
+          // dA (lane = d): lane (i, half) holds column d = 64 dh + 32 dbl + i of
+          // rows n = 8 g + 4 half + e; one q value per column
+          const int lf = fresh_lane();
+          const int hf = lf >> 5, i = lf & 31;
+          float* pw = part + wid * 32 * PRS + i;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) x[e] = row_ok ? qv[e] * dA[2 * dh + dbl][4 * q4 + e] : 0.f;
-            *(floatx4*)(pw + dd) = x;
+          for (int dbl = 0; dbl < 2; ++dbl) {
+            const float qv = (float)*(const bf16*)(qrow + 2 * (64 * dh + 32 * dbl + i));
+            if (nv >= 32) {
+#pragma unroll
+              for (int g4 = 0; g4 < 4; ++g4)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                  pw[(8 * g4 + 4 * hf + e) * PRS + 32 * dbl] = qv * dA[2 * dh + dbl][4 * g4 + e];
+            } else {
+              int nvm = nv;
+              asm volatile("" : "+s"(nvm));
+#pragma unroll
+              for (int g4 = 0; g4 < 4; ++g4)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  const int nr_ = 8 * g4 + 4 * hf + e;
+                  pw[nr_ * PRS + 32 * dbl] = nr_ < nvm ? qv * dA[2 * dh + dbl][4 * g4 + e] : 0.f;
+                }
+            }
           }
+        }
         block_barrier();  // every wave's rows staged
         // thread index from a fresh lane id: the store addresses are not
         // hoisted into registers held through the key loop
