@@ -723,6 +723,9 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_d
   constexpr bool kDK = MODE == 1, kDV = MODE == 2;
   static_assert(kDK || kDV, "one output per launch");
   constexpr int XW = kDK ? DK : DV;  // width of the gradient accumulated
+  // G / O'' with the lane on d (MFMA operands swapped) at score width 256:
+  // the epilogue sums the rows in registers, as the dq pass does there
+  constexpr bool kOT = !F32 && DK >= 256;
   constexpr int NW = NQ * NH;
   constexpr int ROWS = kChunk + NQ - 1;
   constexpr int EW = F32 ? 2 : 1;  // bf16 units per element of an LDS row
@@ -943,15 +946,57 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_d
         }
         const bf16x8 b0 = __builtin_bit_cast(bf16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
         const bf16x8 b1 = __builtin_bit_cast(bf16x8, u32x4{pk[4], pk[5], pk[6], pk[7]});
-        if constexpr (kDK) OPK::template tr_acc<G::RSK>(acc, slot, qo, lane, b0, b1);  // G^T += K2^T · dS^T
-        else OPV::template tr_acc<G::RSV, kPF>(acc, slot + G::VOFF, qo, lane, b0, b1);  // O''^T += V2^T · P^T
+        if constexpr (kDK) OPK::template tr_acc<G::RSK, 1, kOT>(acc, slot, qo, lane, b0, b1);  // G^T += K2^T · dS^T
+        else OPV::template tr_acc<G::RSV, kPF, kOT>(acc, slot + G::VOFF, qo, lane, b0, b1);  // O''^T += V2^T · P^T
       }
       wait_vmcnt<0>();
       block_barrier();  // ring reads done (LDS reused below)
 
       // dk1[d] += Σ_t G_t[d] q_t[d] (MODE 1), dv1[d] += Σ_t O''_t[d] dout_t[d] (MODE 2)
-      float* red = (float*)lds + wid * (64 * 36);
-      {
+      if constexpr (kOT) {
+        // acc (lane = d): column d = 32 db + lane % 32, register 4 g + e = row
+        // n = 8 g + 4 half + e (row-slot row qo + n); the q / dout values read
+        // transposed from the row slot; rows past the window dropped (their
+        // products are 0, and a stale row need not be finite)
+        const int nv = jvalid ? max(0, min(min(32, p.ws - 32 * r), send - (j + 32 * r))) : 0;
+        const int lf = fresh_lane();
+        const int hf = lf >> 5, g16 = (lf >> 4) & 1, i16 = lf & 15;
+        constexpr int RSX = kDK ? G::RSK : G::RSV;
+        const uint32_t xp = lds_addr(rslot + (kDK ? 0 : G::VOFF) + (qo + 4 * hf + (i16 >> 2)) * RSX + 32 * g16 +
+                                     8 * (i16 & 3));
+        static_for<0, XW / 32>([&](auto dd) {
+          constexpr int db = decltype(dd)::value;
+          shortx4 x[4];
+          static_for<0, 4>([&](auto gg) {
+            constexpr int gi = decltype(gg)::value;
+            x[gi] = ds_read_tr16<8 * gi * RSX + 64 * db>(xp);
+          });
+          lds_wait(x[0], x[1]);
+          lds_wait(x[2], x[3]);
+          float sx = 0.f;
+          if (nv >= 32) {
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) sx = fmaf(bf16_bits_to_f32(x[g4][e]), acc[db][4 * g4 + e], sx);
+          } else {
+            // an opaque copy of nv keeps the row tests inside this rare branch
+            int nvm = nv;
+            asm volatile("" : "+s"(nvm));
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const float xv = 8 * g4 + 4 * hf + e < nvm ? bf16_bits_to_f32(x[g4][e]) : 0.f;
+                sx = fmaf(xv, acc[db][4 * g4 + e], sx);
+              }
+          }
+          // both halves hold column d's sum; the half of block db's parity keeps it
+          const float tot = pair_sum(sx);
+          xrun[db >> 1] = hf == (db & 1) ? xrun[db >> 1] + tot : xrun[db >> 1];
+        });
+      } else {
+        float* red = (float*)lds + wid * (64 * 36);
         const char* xs = kDK ? rslot + srow * G::RSK : rslot + G::VOFF + srow * G::RSV;
         floatx4 xv[XW / 64][2][4];
 #pragma unroll
