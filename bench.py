@@ -19,10 +19,12 @@ D=128, long window w1=512, short window w2=32), effective FLOPs
   * beside every nominal prefill figure, ``valid_pair_flops`` and
     ``valid_pair_tflops``: the FLOPs of the (short key, long key) pairs the
     queries can actually see (windows cut at sequence starts), counted in
-    closed form as the reference's cost ledger does (limite_cost.py:31-45, :69-73).
+    closed form as the reference's cost ledger does (limite_cost.py:31-45, :69-73);
+  * ``copy_calibration``: a 1 GiB device copy, this GPU's achievable HBM
+    rate, also set beside the decode rate (``decode.achievable_copy_gbs``).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-                       [--legs prefill,configs,decode,fp32,backward,cpu]
+                       [--legs prefill,configs,decode,global,fp32,backward,det,copy,cpu]
 """
 
 from __future__ import annotations
@@ -50,7 +52,7 @@ def _args():
     ap.add_argument("--decode-steps", type=int, default=200)
     ap.add_argument("--bwd-steps", type=int, default=10)
     ap.add_argument("--bwd-configs", default="C3,C4", help="further workloads of the backward leg")
-    ap.add_argument("--legs", default="prefill,configs,decode,global,fp32,backward,det,cpu")
+    ap.add_argument("--legs", default="prefill,configs,decode,global,fp32,backward,det,copy,cpu")
     ap.add_argument("--configs", default="C2,C3,C4", help="prefill configurations of the configs leg")
     ap.add_argument("--workload", default="NS", help="prefill workload: NS, C2, C3, C4")
     ap.add_argument("--cpu-positions", type=int, default=256)
@@ -550,7 +552,12 @@ def main():
         out["determinant_ds512"] = determinant_leg(args)
         _progress(f"DS 512 / DV 256: {out['determinant_ds512']['ms_per_step']} ms")
     if "copy" in legs:
-        out["copy_calibration"] = copy_leg(args)
+        out["copy_calibration"] = copy = _rounded(copy_leg(args))
+        if "decode" in out:
+            # the decode rate next to the achievable copy rate of this GPU
+            out["decode"]["achievable_copy_gbs"] = copy["gbs"]
+            out["decode"]["frac_of_achievable_copy"] = round(out["decode"]["achieved_gbs"] / copy["gbs"], 4)
+        _progress(f"copy: {copy['gbs']:.0f} GB/s")
     if "cpu" in legs:
         cfg = pre["cfg"] if pre is not None else W.NS
         out["cpu_baseline"] = cpu_leg(args, cfg)
