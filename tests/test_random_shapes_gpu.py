@@ -2,6 +2,10 @@
 against the fp64 oracle (oracle/simplicial_oracle.py, the restatement of
 reference_simplicial, archlab/architectures/simplicial_attention.py:49-74).
 
+The paged (serving) forward gets the same treatment on drawn page sizes,
+contexts, windows and layouts (restating the reference's paged test plan,
+tests/test_simplicial_paged.py, over random geometries).
+
 The shapes are drawn from a fixed seed so that every run checks the same
 cases: batch 1-2 (or packed sequences), 1-180 tokens, KV heads 1-4, GQA
 groups 1-4, score / value widths 64, 128 and 256 (equal or not where the
@@ -22,7 +26,7 @@ import random
 import pytest
 import torch
 
-from helpers import rand_inputs
+from helpers import paged_batch, rand_inputs
 from oracle import simplicial_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -139,3 +143,55 @@ def test_random_packed_sequences_backward_bf16(cuda, case):
     for name, tg, r in zip(("dq", "dk1", "dk2", "dv1", "dv2"), xd, xs):
         errs.append(_check(f"{label} {name}", tg.grad, r.grad.float(), 2e-2))
     print(label + ": " + " ".join(f"{e:.1e}" for e in errs), flush=True)
+
+
+def _draw_paged(rng):
+    dim = rng.choice([64, 128, 128, 256])
+    kv_heads = rng.choice([1, 2, 4])
+    group = rng.choice([1, 2, 4, 8])
+    block = rng.choice([16, 64])
+    lengths = [rng.randint(1, 1500) for _ in range(rng.randint(1, 4))]
+    ws = rng.choice([1, 4, 16, 32, 40, 64])
+    wl = max(ws, rng.choice([ws, 64, 300, 1 << 30]))
+    qdt = rng.choice([torch.bfloat16, torch.float32])
+    hnd = rng.random() < 0.5
+    return dim, kv_heads, group, block, lengths, ws, wl, qdt, hnd
+
+
+_PAGED = [_draw_paged(random.Random(4000 + i)) for i in range(16)]
+
+
+@pytest.mark.parametrize("case", range(len(_PAGED)))
+def test_random_paged_decode_and_prefill_tokens(cuda, case):
+    """Paged forward on drawn geometries (bf16 caches in NHD or HND layout,
+    shuffled pages, a null block, bf16 or fp32 queries, windows up to global
+    ones that clip to the block tables' reach) for each sequence's last token
+    and two earlier positions, against the dense oracle on the same rows."""
+    from archlab_amd import simplicial_paged_attention
+    dim, kv_heads, group, block, lengths, ws, wl, qdt, hnd = _PAGED[case]
+    heads = kv_heads * group
+    (short, long), table, dense = paged_batch(lengths, kv_heads, dim, block, torch.bfloat16, hnd, seed=case,
+                                              device=cuda)
+    rng = random.Random(5000 + case)
+    g = torch.Generator().manual_seed(6000 + case)
+    seqs, positions, queries, expected = [], [], [], []
+    for s, (n, (k1, k2, v1, v2)) in enumerate(zip(lengths, dense)):
+        q = (torch.randn(1, n, heads, dim, generator=g) / dim ** 0.5).to(qdt)
+        chosen = sorted({n - 1, rng.randrange(n), rng.randrange(n)})
+        ref = O.reference_simplicial(q.double(), k1.double(), k2.double(), v1.double(), v2.double(), ws, wl,
+                                     scale=1.0, query_positions=chosen)
+        for i, position in enumerate(chosen):
+            seqs.append(s)
+            positions.append(position)
+            queries.append(q[0, position])
+            expected.append(ref[0, i])
+    q = torch.stack(queries).to(cuda)
+    seq = torch.tensor(seqs, dtype=torch.int32, device=cuda)
+    pos = torch.tensor(positions, dtype=torch.int32, device=cuda)
+    out = simplicial_paged_attention(q, short, long, table, seq, pos, short_window=ws, long_window=wl, scale=1.0)
+    tol = 2e-4 if qdt == torch.float32 else 3e-2
+    exp = torch.stack(expected).float()
+    err = (out.cpu() - exp).abs().max().item()
+    print(f"paged case {case}: d{dim} h{heads}/{kv_heads} block {block} lengths {lengths} w{ws}x{wl} "
+          f"{qdt} hnd={hnd}: {err:.2e}", flush=True)
+    torch.testing.assert_close(out.cpu(), exp, rtol=tol, atol=tol)
