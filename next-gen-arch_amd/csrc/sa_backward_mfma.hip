@@ -38,11 +38,12 @@ namespace sa {
 
 namespace {
 
-// LDS fragments read ahead of their MFMA in each pass (see BwdOps); at score
-// width 256 (one wave per SIMD: no other wave hides the LDS latency) the dq
-// and dk2 / dv2 passes read further ahead (C4 forward + backward 29.1 ->
-// 28.7 and 28.9 ms)
-constexpr int kDqPF = 1, kDqPFWide = 3;      // dq pass
+// LDS fragments read ahead of their MFMA in each pass (see BwdOps; dq two
+// ahead at widths up to 128: NS forward + backward 17.05 -> 16.96 ms, the
+// adapter shape 8.85 -> 8.74 ms); at score width 256 (one wave per SIMD: no
+// other wave hides the LDS latency) the dq and dk2 / dv2 passes read further
+// ahead (C4 forward + backward 29.1 -> 28.7 and 28.9 ms)
+constexpr int kDqPF = 2, kDqPFWide = 3;      // dq pass
 constexpr int kDk1PF = 1;                    // dk1 / dv1 pass (dv1 reads two ahead)
 constexpr int kDkv2PF = 2, kDkv2PFWide = 4;  // dk2 / dv2 pass
 
