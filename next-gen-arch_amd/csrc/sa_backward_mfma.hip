@@ -66,11 +66,16 @@ struct BwdOps {
     const char* kp = tile + (row0 + n) * RS + 16 * half;
     floatx16 c = floatx16{};
     if constexpr (PF > 1) {
+      // explicit reads and counted waits (the compiler's waits for plain
+      // loads here would also wait for the reads issued ahead)
+      const uint32_t ka = lds_addr(kp);
       bf16x8 f[D / 16];
-      static_for<0, (PF < D / 16 ? PF : D / 16)>([&](auto s) { f[s] = *(const bf16x8*)(kp + 32 * s); });
+      static_for<0, (PF < D / 16 ? PF : D / 16)>(
+          [&](auto s) { f[s] = ds_read_b128_at<32 * decltype(s)::value>(ka); });
       static_for<0, D / 16>([&](auto st) {
         constexpr int s = decltype(st)::value;
-        if constexpr (s + PF < D / 16) f[s + PF] = *(const bf16x8*)(kp + 32 * (s + PF));
+        if constexpr (s + PF < D / 16) f[s + PF] = ds_read_b128_at<32 * (s + PF)>(ka);
+        lds_wait_k<(s + PF < D / 16 ? s + PF : D / 16 - 1) - s>(f[s]);  // reads issued after f[s]'s
         __builtin_amdgcn_sched_barrier(0);
         c = mfma32x32x16(f[s], x[s], c);
         __builtin_amdgcn_sched_barrier(0);

@@ -186,6 +186,25 @@ __device__ __forceinline__ void lds_wait_n(shortx4& a, shortx4& b) {
   asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
 }
 
+// ds_read_b128 issued through inline asm, for fragment chains that read ahead
+// of their MFMAs: for the compiler's own reads in such a chain the backend
+// emits lgkmcnt(0) before every few MFMAs, which also waits for the reads
+// issued ahead (one MFMA earlier), so the chain stalls on LDS latency.  The
+// result is only valid after lds_wait_k on it, with the exact count of LDS
+// operations issued after it.
+template <int OFF>
+__device__ __forceinline__ bf16x8 ds_read_b128_at(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "16-bit LDS offset");
+  bf16x8 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+template <int N>
+__device__ __forceinline__ void lds_wait_k(bf16x8& a) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt is 4 bits");
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "i"(N));
+}
+
 // Row sum of one chunk's probabilities beyond which the chunk loop moves the
 // reference max (see RowBlock::chunk): probabilities stay below 2^24, far
 // inside the fp32 range of the accumulators, and bf16 rounding is relative.
@@ -485,15 +504,18 @@ struct RowBlock {
       } else {
         bf16x8 kq[DK / 16];
         constexpr int KA = DK >= 512 ? 4 : 2;  // fragments read ahead
-#pragma unroll
-        for (int t = 0; t < KA && t < DK / 16; ++t) kq[t] = *(const bf16x8*)(kp + 32 * t);
-#pragma unroll
-        for (int t = 0; t < DK / 16; ++t) {
-          if (t + KA < DK / 16) kq[t + KA] = *(const bf16x8*)(kp + 32 * (t + KA));
+        // explicit reads and counted waits (ds_read_b128_at)
+        const uint32_t ka = lds_addr(kp);
+        static_for<0, (KA < DK / 16 ? KA : DK / 16)>(
+            [&](auto tt) { kq[tt] = ds_read_b128_at<32 * decltype(tt)::value>(ka); });
+        static_for<0, DK / 16>([&](auto tt) {
+          constexpr int t = decltype(tt)::value;
+          if constexpr (t + KA < DK / 16) kq[t + KA] = ds_read_b128_at<32 * (t + KA)>(ka);
+          lds_wait_k<(t + KA < DK / 16 ? t + KA : DK / 16 - 1) - t>(kq[t]);
           __builtin_amdgcn_sched_barrier(0);
           s = qk_mfma(kq[t], t, s);
           __builtin_amdgcn_sched_barrier(0);
-        }
+        });
       }
     }
     const bool masked = key_lo > 0 || key_hi < kChunk - 1;
