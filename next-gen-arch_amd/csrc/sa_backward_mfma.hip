@@ -1141,8 +1141,8 @@ __global__ __launch_bounds__(256) void bwd_dk1_sum_kernel(BwdParams p, int qbloc
 // j = t - 32r - 31 .. t - 32r: bf16(q_th ⊙ k1_j)) and B_t (bf16(dout_th ⊙
 // v1_j)) in LDS, 32 / NWK rows each; tiles are double-buffered, one barrier
 // per step.  Wider blocks (NWK = 8 at D = 128) share each step's tile
-// formation, barrier and staging among more keys.  Wave 0 stages each step's
-// q, dout, k1_t and v1_t rows with one full-wave DMA two steps ahead; the
+// formation, barrier and staging among more keys.  The last wave stages each
+// step's q, dout, k1_t and v1_t rows with one full-wave DMA two steps ahead; the
 // k1 / v1 rows of earlier queries come from a 64·NR-row ring (row j at slot
 // j % (64 NR)) into which wave 0 copies each staged k1_t / v1_t.  Covers
 // ws <= 32 NR (NR = 1, 2).
@@ -1328,25 +1328,34 @@ __global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_
     if (y.h == g * G + G) y.h = g * G, ++y.t;
     return y;
   };
-  // Wave 0 stages step st: lane -> byte 16 lane of the rows q, dout, k1_t, v1_t
-  // laid end to end (lanes past them re-fetch the q row's first segment into
-  // the unused tail); every lane active, one instruction.
+  // The staging wave stages step st: lane -> byte 16 lane of the rows q,
+  // dout, k1_t, v1_t laid end to end (lanes past them re-fetch the q row's
+  // first segment into the unused tail); every lane active, one instruction
+  // per 1 KB.  Every wave waits for the staging wave at the step's barrier, so
+  // its addresses are selected per lane without branches (a lane's tensor is
+  // fixed by its byte offset b), the row offsets formed once per step in
+  // scalars.  Four-wave workgroups stage from the last wave (wave 0 copies
+  // rows into the ring): dk2 / dv2 3-4 % faster at the adapter shape and at
+  // width 256 than from wave 0; eight-wave ones from wave 0 (the last wave
+  // measured 4 % slower there).
+  constexpr int kDmaWave = NWK >= 8 ? 0 : NWK - 1;
   auto dma_step = [&](int st, Step x) {
-    if (wid != 0 || st >= nsteps) return;
-    const int t = x.t, h = x.h;
+    if (wid != kDmaWave || st >= nsteps) return;
+    // element offsets of the step's rows (uniform)
+    const int64_t oq = (int64_t)x.t * p.q_st + (int64_t)x.h * p.q_sh;
+    const int64_t og = (int64_t)x.t * p.do_st + (int64_t)x.h * p.do_sh;
+    const int64_t ok = (int64_t)x.t * p.k_st + kvg_k, ov = (int64_t)x.t * p.v_st + kvg_v;
 #pragma unroll
     for (int k = 0; k < SI; ++k) {
       // byte offset from a fresh lane id: not hoisted into registers held through the step loop
       int b = 1024 * k + 16 * fresh_lane();
       if (b >= 2 * RKV) b = 0;
-      const bf16* src;
+      const bool isq = b < RBK, isg = b < RKV, isk = b < RKV + RBK;
+      const bf16* base = isq ? (const bf16*)p.q : isg ? (const bf16*)p.dout : isk ? (const bf16*)p.k1 : (const bf16*)p.v1;
+      const int64_t oe = isq ? oq : isg ? og : isk ? ok : ov;
+      const int inrow = b - (isq ? 0 : isg ? RBK : isk ? RKV : RKV + RBK);  // bytes
       // (element offsets scaled by EW: fp32 rows viewed as bf16 units)
-      if (b < RBK) src = (const bf16*)p.q + EW * ((int64_t)t * p.q_st + (int64_t)h * p.q_sh) + b / 2;
-      else if (b < RKV)
-        src = (const bf16*)p.dout + EW * ((int64_t)t * p.do_st + (int64_t)h * p.do_sh) + (b - RBK) / 2;
-      else if (b < RKV + RBK) src = (const bf16*)p.k1 + EW * ((int64_t)t * p.k_st + kvg_k) + (b - RKV) / 2;
-      else src = (const bf16*)p.v1 + EW * ((int64_t)t * p.v_st + kvg_v) + (b - RKV - RBK) / 2;
-      dma16(src, stage + x.slot * SS + 1024 * k);
+      dma16(base + EW * oe + inrow / 2, stage + x.slot * SS + 1024 * k);
     }
   };
   // wave 0 copies the staged k1_t / v1_t rows of step st into ring slot t % (64 NR)
@@ -1515,8 +1524,8 @@ __global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_
       store_block();
       if (st + 64 < nsteps) load_block((st >> 6) + 1);
     }
-    // wave 0: the rows of step st+1 have landed (step st+2's may be in flight)
-    if (wid == 0) {
+    // staging wave: the rows of step st+1 have landed (step st+2's may be in flight)
+    if (wid == kDmaWave) {
       dma_step(st + 2, s_nx2);
       if (st + 2 < nsteps) wait_vmcnt<SI>();
       else wait_vmcnt<0>();
