@@ -547,15 +547,23 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_d
       const int lf = fresh_lane();
       const int hf = lf >> 5, g16 = (lf >> 4) & 1, i16 = lf & 15;
       const uint32_t k1p = lds_addr(sslot + (qo + 7 - 4 * hf - (i16 >> 2)) * G::RSK + 32 * g16 + 8 * (i16 & 3));
-      static_for<0, DK / 32>([&](auto dd) {
+      // the k1 values of block db + 1 are read while block db is summed
+      shortx4 xb[DK / 32][4];
+      auto read_k1 = [&](auto dd) {
         constexpr int db = decltype(dd)::value;
-        shortx4 x[4];
         static_for<0, 4>([&](auto gg) {
           constexpr int gi = decltype(gg)::value;
-          x[gi] = ds_read_tr16<(24 - 8 * gi) * G::RSK + 64 * db>(k1p);
+          xb[db][gi] = ds_read_tr16<(24 - 8 * gi) * G::RSK + 64 * db>(k1p);
         });
-        lds_wait(x[0], x[1]);
-        lds_wait(x[2], x[3]);
+      };
+      read_k1(std::integral_constant<int, 0>{});
+      static_for<0, DK / 32>([&](auto dd) {
+        constexpr int db = decltype(dd)::value;
+        if constexpr (db + 1 < DK / 32) read_k1(std::integral_constant<int, db + 1>{});
+        shortx4* const x = xb[db];
+        constexpr int kLater = db + 1 < DK / 32 ? 4 : 0;  // reads issued after block db's
+        lds_wait_n<kLater>(x[0], x[1]);
+        lds_wait_n<kLater>(x[2], x[3]);
         float acc = 0.f;
         if (nv >= 32) {
 #pragma unroll
@@ -588,74 +596,86 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_d
       // every (jrow, 4 d) over its waves in wave order and writes it.
       constexpr int PRS = 68;                   // staged row stride (floats)
       constexpr int ROWS1 = 31 + NQ;            // partial rows
+      // 64-wide d halves staged per round: two where the ring region holds
+      // them (widths of 256: half the rounds, barriers and LDS latencies; at
+      // score width 256 over value width 128 the allocator then spills, so
+      // one there)
+      constexpr int kPart = NW * 32 * PRS;      // floats of one staged half
+      constexpr int DHR = RING / (4 * kPart) >= 2 && DK / 64 >= 2 && DV == DK ? 2 : 1;
+      static_assert((DK / 64) % DHR == 0 && DHR * 4 * kPart <= RING, "staged halves fit the ring region");
       const char* qrow = qslot + wid * G::RSK;  // q row of this wave's (t, h)
-      float* part = (float*)lds;                // [NW][32][PRS] (ring region)
       float* const dst = p.dk1p + (((int64_t)hg * geo.qblocks + qb) * geo.nr + r) * (ROWS1 * DK);
 #pragma unroll
-      for (int dh = 0; dh < DK / 64; ++dh) {
-        if constexpr (!kOT) {
-          // dA^T: lane n holds row n, 4 consecutive d per 16-byte write
-          float* pw = part + (wid * 32 + (fresh_lane() & 31)) * PRS;
+      for (int dr = 0; dr < DK / 64; dr += DHR) {
 #pragma unroll
-          for (int dbl = 0; dbl < 2; ++dbl)
+        for (int dh = dr; dh < dr + DHR; ++dh) {
+          float* const part = (float*)lds + (dh - dr) * kPart;  // [NW][32][PRS] (ring region)
+          if constexpr (!kOT) {
+            // dA^T: lane n holds row n, 4 consecutive d per 16-byte write
+            float* pw = part + (wid * 32 + (fresh_lane() & 31)) * PRS;
 #pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-              const int dd = 32 * dbl + 8 * q4 + 4 * half;
-              floatx4 qv;
-              if constexpr (F32) {
-                qv = *(const floatx4*)(qrow + 4 * (64 * dh + dd));
-              } else {
-                const bf16x4 qb4 = *(const bf16x4*)(qrow + 2 * (64 * dh + dd));
+            for (int dbl = 0; dbl < 2; ++dbl)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) qv[e] = (float)qb4[e];
-              }
-              floatx4 x;
+              for (int q4 = 0; q4 < 4; ++q4) {
+                const int dd = 32 * dbl + 8 * q4 + 4 * half;
+                floatx4 qv;
+                if constexpr (F32) {
+                  qv = *(const floatx4*)(qrow + 4 * (64 * dh + dd));
+                } else {
+                  const bf16x4 qb4 = *(const bf16x4*)(qrow + 2 * (64 * dh + dd));
 #pragma unroll
-              for (int e = 0; e < 4; ++e) x[e] = row_ok ? qv[e] * dA[2 * dh + dbl][4 * q4 + e] : 0.f;
-              *(floatx4*)(pw + dd) = x;
-            }
-        } else {
-          // dA (lane = d): lane (i, half) holds column d = 64 dh + 32 dbl + i of
-          // rows n = 8 g + 4 half + e; one q value per column
-          const int lf = fresh_lane();
-          const int hf = lf >> 5, i = lf & 31;
-          float* pw = part + wid * 32 * PRS + i;
-#pragma unroll
-          for (int dbl = 0; dbl < 2; ++dbl) {
-            const float qv = (float)*(const bf16*)(qrow + 2 * (64 * dh + 32 * dbl + i));
-            if (nv >= 32) {
-#pragma unroll
-              for (int g4 = 0; g4 < 4; ++g4)
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                  pw[(8 * g4 + 4 * hf + e) * PRS + 32 * dbl] = qv * dA[2 * dh + dbl][4 * g4 + e];
-            } else {
-              int nvm = nv;
-              asm volatile("" : "+s"(nvm));
-#pragma unroll
-              for (int g4 = 0; g4 < 4; ++g4)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                  const int nr_ = 8 * g4 + 4 * hf + e;
-                  pw[nr_ * PRS + 32 * dbl] = nr_ < nvm ? qv * dA[2 * dh + dbl][4 * g4 + e] : 0.f;
+                  for (int e = 0; e < 4; ++e) qv[e] = (float)qb4[e];
                 }
+                floatx4 x;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) x[e] = row_ok ? qv[e] * dA[2 * dh + dbl][4 * q4 + e] : 0.f;
+                *(floatx4*)(pw + dd) = x;
+              }
+          } else {
+            // dA (lane = d): lane (i, half) holds column d = 64 dh + 32 dbl + i of
+            // rows n = 8 g + 4 half + e; one q value per column
+            const int lf = fresh_lane();
+            const int hf = lf >> 5, i = lf & 31;
+            float* pw = part + wid * 32 * PRS + i;
+#pragma unroll
+            for (int dbl = 0; dbl < 2; ++dbl) {
+              const float qv = (float)*(const bf16*)(qrow + 2 * (64 * dh + 32 * dbl + i));
+              if (nv >= 32) {
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4)
+#pragma unroll
+                  for (int e = 0; e < 4; ++e)
+                    pw[(8 * g4 + 4 * hf + e) * PRS + 32 * dbl] = qv * dA[2 * dh + dbl][4 * g4 + e];
+              } else {
+                int nvm = nv;
+                asm volatile("" : "+s"(nvm));
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4)
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) {
+                    const int nr_ = 8 * g4 + 4 * hf + e;
+                    pw[nr_ * PRS + 32 * dbl] = nr_ < nvm ? qv * dA[2 * dh + dbl][4 * g4 + e] : 0.f;
+                  }
+              }
             }
           }
         }
         block_barrier();  // every wave's rows staged
         // thread index from a fresh lane id: the store addresses are not
         // hoisted into registers held through the key loop
-        for (int o = fresh_lane() + 64 * wid; o < ROWS1 * 16; o += 64 * NW) {
-          const int jrow = o >> 4, d4 = o & 15;
+        for (int o = fresh_lane() + 64 * wid; o < DHR * ROWS1 * 16; o += 64 * NW) {
+          const int u = DHR > 1 ? o / (ROWS1 * 16) : 0;
+          const int jrow = (DHR > 1 ? o % (ROWS1 * 16) : o) >> 4, d4 = o & 15;
+          const float* const part = (const float*)lds + u * kPart;
           floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int w = 0; w < NW; ++w) {
             const int nn = w / NH + 31 - jrow;  // wave w = (qo, hw) = (w / NH, w % NH)
             if (nn >= 0 && nn < 32) acc += *(const floatx4*)(part + (w * 32 + nn) * PRS + 4 * d4);
           }
-          *(floatx4*)(dst + jrow * DK + 64 * dh + 4 * d4) = acc;
+          *(floatx4*)(dst + jrow * DK + 64 * (dr + u) + 4 * d4) = acc;
         }
-        block_barrier();  // sums read before the next half (or exit) reuses the region
+        block_barrier();  // sums read before the next round (or exit) reuses the region
       }
     }
   }
