@@ -1446,27 +1446,36 @@ __global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_
       }
     } else if constexpr (DK == DV) {  // A and B rows side by side: one row and segment per lane
       constexpr int SEGS = DK / 8;  // 16-byte segments per row
-      static_assert(RPW * SEGS % 64 == 0, "whole lanes per formed row block");
+      static_assert(RPW * SEGS % 64 == 0 && 64 % SEGS == 0, "whole lanes per formed row block");
+      constexpr int NU = NR * RPW * SEGS / 64;  // row blocks formed by each lane
+      // A lane forms segment sg = lane % SEGS of every row block, so its q and
+      // dout segments are read once; every k1 / v1 read is issued before the
+      // first product (the tile writes would otherwise keep each block's reads
+      // behind the previous block's writes: one LDS latency per block).
+      const int sg = lane % SEGS;
+      const u32x4 q4 = __builtin_bit_cast(u32x4, *(const bf16x8*)(sg_row + 16 * sg));
+      const u32x4 g4 = __builtin_bit_cast(u32x4, *(const bf16x8*)(sg_row + RBK + 16 * sg));
+      u32x4 k4[NU], v4[NU];
 #pragma unroll
-      for (int u = 0; u < NR * RPW * SEGS / 64; ++u) {
+      for (int u = 0; u < NU; ++u) {
         const int r = u / (RPW * SEGS / 64);  // row group
-        char* At = tiles + (b * NR + r) * TAB;
-        char* Bt = At + TA;
-        const int idx = (u % (RPW * SEGS / 64)) * 64 + lane;
-        const int i = RPW * wid + idx / SEGS, sg = idx % SEGS;  // tile row, segment
+        const int i = RPW * wid + ((u % (RPW * SEGS / 64)) * 64 + lane) / SEGS;  // tile row
         const int j = max(t - 32 * (r + r0) - 31 + i, 0);
         const char* kvrow = j == t ? sg_row + RKV : ring + (j % kKvRing) * RKV;
-        const bf16x8 qv = *(const bf16x8*)(sg_row + 16 * sg);
-        const bf16x8 gv = *(const bf16x8*)(sg_row + RBK + 16 * sg);
-        const bf16x8 kv = *(const bf16x8*)(kvrow + 16 * sg);
-        const bf16x8 vv = *(const bf16x8*)(kvrow + RBK + 16 * sg);
-        const u32x4 q4 = __builtin_bit_cast(u32x4, qv), g4 = __builtin_bit_cast(u32x4, gv);
-        const u32x4 k4 = __builtin_bit_cast(u32x4, kv), v4 = __builtin_bit_cast(u32x4, vv);
+        k4[u] = __builtin_bit_cast(u32x4, *(const bf16x8*)(kvrow + 16 * sg));
+        v4[u] = __builtin_bit_cast(u32x4, *(const bf16x8*)(kvrow + RBK + 16 * sg));
+      }
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const int r = u / (RPW * SEGS / 64);
+        char* At = tiles + (b * NR + r) * TAB;
+        char* Bt = At + TA;
+        const int i = RPW * wid + ((u % (RPW * SEGS / 64)) * 64 + lane) / SEGS;
         u32x4 a, bb;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          a[e] = mul_bf16_pair(q4[e], k4[e]);
-          bb[e] = mul_bf16_pair(g4[e], v4[e]);
+          a[e] = mul_bf16_pair(q4[e], k4[u][e]);
+          bb[e] = mul_bf16_pair(g4[e], v4[u][e]);
         }
         *(u32x4*)(At + i * RSA + 16 * sg) = a;
         *(u32x4*)(Bt + i * RSB + 16 * sg) = bb;
