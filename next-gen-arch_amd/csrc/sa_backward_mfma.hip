@@ -1413,36 +1413,48 @@ __global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_
     if constexpr (F32) {
       // fp32 rows: one row and 4 elements (16 source bytes) per lane; the
       // products q ⊙ k1 and dout ⊙ v1 split into hi (row elements 4 sg ..)
-      // and lo (elements D + 4 sg ..) bf16 terms
+      // and lo (elements D + 4 sg ..) bf16 terms.  A lane's 4-element group sg
+      // = lane % SEGS is the same in every row block: its q and dout values
+      // are read once, and the k1 / v1 reads of kB blocks at a time are
+      // issued before their products.
       constexpr int SEGS = DK / 4;
-      static_assert(RPW * SEGS % 64 == 0, "whole lanes per formed row block");
+      static_assert(RPW * SEGS % 64 == 0 && 64 % SEGS == 0, "whole lanes per formed row block");
+      constexpr int NU = RPW * SEGS / 64, kB = NU < 2 ? NU : 2;
+      const int sg = lane % SEGS;
+      const floatx4 qv = *(const floatx4*)(sg_row + 16 * sg);
+      const floatx4 gv = *(const floatx4*)(sg_row + RBK + 16 * sg);
+      char* At = tiles + b * TAB;
+      char* Bt = At + TA;
 #pragma unroll
-      for (int u = 0; u < RPW * SEGS / 64; ++u) {
-        char* At = tiles + b * TAB;
-        char* Bt = At + TA;
-        const int idx = u * 64 + lane;
-        const int i = RPW * wid + idx / SEGS, sg = idx % SEGS;  // tile row, 4-element group
-        const int j = max(t - 31 + i, 0);
-        const char* kvrow = j == t ? sg_row + RKV : ring + (j % kKvRing) * RKV;
-        const floatx4 qv = *(const floatx4*)(sg_row + 16 * sg);
-        const floatx4 gv = *(const floatx4*)(sg_row + RBK + 16 * sg);
-        const floatx4 kv = *(const floatx4*)(kvrow + 16 * sg);
-        const floatx4 vv = *(const floatx4*)(kvrow + RBK + 16 * sg);
-        bf16x4 ah, al, bh, bl;
+      for (int u0 = 0; u0 < NU; u0 += kB) {
+        floatx4 kv[kB], vv[kB];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          bf16 h_, l_;
-          split_bf16(qv[e] * kv[e], h_, l_);
-          ah[e] = h_;
-          al[e] = l_;
-          split_bf16(gv[e] * vv[e], h_, l_);
-          bh[e] = h_;
-          bl[e] = l_;
+        for (int u = 0; u < kB; ++u) {
+          const int i = RPW * wid + ((u0 + u) * 64 + lane) / SEGS;  // tile row
+          const int j = max(t - 31 + i, 0);
+          const char* kvrow = j == t ? sg_row + RKV : ring + (j % kKvRing) * RKV;
+          kv[u] = *(const floatx4*)(kvrow + 16 * sg);
+          vv[u] = *(const floatx4*)(kvrow + RBK + 16 * sg);
         }
-        *(bf16x4*)(At + i * RSA + 8 * sg) = ah;
-        *(bf16x4*)(At + i * RSA + 2 * DK + 8 * sg) = al;
-        *(bf16x4*)(Bt + i * RSB + 8 * sg) = bh;
-        *(bf16x4*)(Bt + i * RSB + 2 * DV + 8 * sg) = bl;
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+          const int i = RPW * wid + ((u0 + u) * 64 + lane) / SEGS;
+          bf16x4 ah, al, bh, bl;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            bf16 h_, l_;
+            split_bf16(qv[e] * kv[u][e], h_, l_);
+            ah[e] = h_;
+            al[e] = l_;
+            split_bf16(gv[e] * vv[u][e], h_, l_);
+            bh[e] = h_;
+            bl[e] = l_;
+          }
+          *(bf16x4*)(At + i * RSA + 8 * sg) = ah;
+          *(bf16x4*)(At + i * RSA + 2 * DK + 8 * sg) = al;
+          *(bf16x4*)(Bt + i * RSB + 8 * sg) = bh;
+          *(bf16x4*)(Bt + i * RSB + 2 * DV + 8 * sg) = bl;
+        }
       }
     } else if constexpr (DK == DV) {  // A and B rows side by side: one row and segment per lane
       constexpr int SEGS = DK / 8;  // 16-byte segments per row
@@ -1482,10 +1494,16 @@ __global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_
       }
     } else {  // A rows (DK / 8 segments), then B rows (DV / 8)
       constexpr int SK = DK / 8, SV = DV / 8;
-      static_assert(RPW * SK % 64 == 0 && RPW * SV % 64 == 0, "whole lanes per formed row block");
-      constexpr int UA = RPW * SK / 64, UB = RPW * SV / 64;
+      static_assert(RPW * SK % 64 == 0 && RPW * SV % 64 == 0 && 64 % SK == 0 && 64 % SV == 0,
+                    "whole lanes per formed row block");
+      constexpr int UA = RPW * SK / 64, UB = RPW * SV / 64, NU = NR * (UA + UB);
+      // as above: a lane's q (dout) segment lane % SK (lane % SV) is the same
+      // in every A (B) block, read once; every k1 / v1 read is issued first
+      const u32x4 q4 = __builtin_bit_cast(u32x4, *(const bf16x8*)(sg_row + 16 * (lane % SK)));
+      const u32x4 g4 = __builtin_bit_cast(u32x4, *(const bf16x8*)(sg_row + RBK + 16 * (lane % SV)));
+      u32x4 y4[NU];
 #pragma unroll
-      for (int u = 0; u < NR * (UA + UB); ++u) {
+      for (int u = 0; u < NU; ++u) {
         const int r = u / (UA + UB), v = u % (UA + UB);  // row group, instruction within it
         const bool isb = v >= UA;
         const int segs = isb ? SV : SK, off = isb ? RBK : 0;
@@ -1493,11 +1511,19 @@ __global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_
         const int i = RPW * wid + idx / segs, sg = idx % segs;  // tile row, segment
         const int j = max(t - 32 * (r + r0) - 31 + i, 0);
         const char* kvrow = j == t ? sg_row + RKV : ring + (j % kKvRing) * RKV;
-        const u32x4 x4 = __builtin_bit_cast(u32x4, *(const bf16x8*)(sg_row + off + 16 * sg));
-        const u32x4 y4 = __builtin_bit_cast(u32x4, *(const bf16x8*)(kvrow + off + 16 * sg));
+        y4[u] = __builtin_bit_cast(u32x4, *(const bf16x8*)(kvrow + off + 16 * sg));
+      }
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const int r = u / (UA + UB), v = u % (UA + UB);
+        const bool isb = v >= UA;
+        const int segs = isb ? SV : SK;
+        const int idx = (isb ? v - UA : v) * 64 + lane;
+        const int i = RPW * wid + idx / segs, sg = idx % segs;
+        const u32x4 x4 = isb ? g4 : q4;
         u32x4 a;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) a[e] = mul_bf16_pair(x4[e], y4[e]);
+        for (int e = 0; e < 4; ++e) a[e] = mul_bf16_pair(x4[e], y4[u][e]);
         char* At = tiles + (b * NR + r) * TAB;
         *(u32x4*)(isb ? At + TA + i * RSB + 16 * sg : At + i * RSA + 16 * sg) = a;
       }
