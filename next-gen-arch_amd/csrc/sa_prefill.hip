@@ -96,9 +96,9 @@ void prefill_mfma_kernel(PrefillParams p) {
   constexpr int NI = G::NI;
   extern __shared__ __attribute__((aligned(16))) char lds[];
   // The pass's v1 rows (rows kbs.. in the V-tile layout, read by the row
-  // merge): placed so that their V region is the free ring slot or the area
-  // after the ring.
-  char* const v1slot = kV1Ring ? lds + (p.nc % R) * G::SLOT : lds + R * G::SLOT - G::VOFF;
+  // merge): placed so that their V region is the area after the ring (widths
+  // up to 128; otherwise a ring slot chosen per pass, below).
+  char* const v1slot = lds + R * G::SLOT - G::VOFF;
   // bf16 widths up to 128: the A-row inputs are staged in LDS (k1 rows in the
   // K region, q rows in the V region of a free ring slot; at 256 the staged
   // form costs the kernel register spills)
@@ -217,6 +217,18 @@ void prefill_mfma_kernel(PrefillParams p) {
   float Mrun = -INFINITY, Zrun = 0.f;
 
   for (int r = 0; r < p.nr; ++r) {
+    // Passes alternate the direction of their chunk walk (even passes
+    // ascending, odd ones descending), so that every pass after the first
+    // starts on the tile the previous one ended with, still in its ring slot:
+    // no DMA and no wait for it.  The direction changes only the order of the
+    // online softmax's sums, which is fixed for a given shape.
+    const bool rev = (r & 1) != 0;                // uniform
+    const int cf = rev ? p.nc - 1 : c0;           // first chunk of the pass
+    const int cl = rev ? c0 : p.nc - 1;           // last chunk of the pass
+    const bool resident = r > 0 && c0 < p.nc;     // first tile already in LDS
+    // widths of 256 / fp32: the pass's v1 rows go to the slot that does not
+    // hold its last chunk (free while that chunk is processed)
+    char* const v1s = kV1Ring ? slot_of(cl + 1) : v1slot;
     // lane-derived values from a fresh lane index: computed per pass, not
     // kept (or spilled) through the key loops of a multi-pass query
     const int lp = fresh_lane();
@@ -239,7 +251,7 @@ void prefill_mfma_kernel(PrefillParams p) {
     // the first tile, and the A rows are formed from LDS while the tile
     // streams (vector loads would retire behind the tile's DMA, and each wave
     // would fetch its own overlapping k1 rows)
-    char* const kslot = slot_of(c0 + 1);
+    char* const kslot = slot_of(cf + 1);
     char* const qslot = kslot + G::VOFF;
     if constexpr (kStageA) {
       dma_tile(std::integral_constant<int, 1>{}, kslot, kbs, (const bf16*)p.k1, p.v1);
@@ -254,9 +266,11 @@ void prefill_mfma_kernel(PrefillParams p) {
         }
       }
     }
-    issue(c0);
+    if (!resident) issue(cf);
     if constexpr (kStageA) {
-      wait_vmcnt<G::NI>();  // the staged rows (the tile may still be in flight)
+      // the staged rows (the first tile, when issued, may still be in flight)
+      if (resident) wait_vmcnt<0>();
+      else wait_vmcnt<G::NI>();
       block_barrier();
       // lane n's k1 row j = t - 32r - n is slot row qo + 31 - n; rows outside
       // the window are masked
@@ -282,15 +296,18 @@ void prefill_mfma_kernel(PrefillParams p) {
       // Tile addresses of the chunk issued next, advanced by one chunk per
       // step (no 64-bit multiply in the loop); used when the tile lies inside
       // the tensor, the general tile DMA otherwise.
-      const int64_t kstep = (int64_t)kChunk * k_st * 2, vstep = (int64_t)kChunk * v_st * 2;
-      int kbn = kb0 + kChunk * (c0 + 1);  // key of the next tile's row 0
+      const int dir = rev ? -1 : 1;
+      const int64_t kstep = dir * (int64_t)kChunk * k_st * 2, vstep = dir * (int64_t)kChunk * v_st * 2;
+      int kbn = kb0 + kChunk * (cf + dir);  // key of the next tile's row 0
       const char* kn = (const char*)(p.k2 + k_g) + (int64_t)kbn * k_st * 2;
       const char* vn = (const char*)(p.v2 + v_g) + (int64_t)kbn * v_st * 2;
-      for (int c = c0; c < p.nc; ++c) {
+      const int nsteps = p.nc - c0;
+      for (int i = 0; i < nsteps; ++i) {
+        const int c = cf + dir * i;
         wait_vmcnt<0>();
-        block_barrier();  // tile c complete for every wave; slot of tile c-1 free
-        if (c + 1 < p.nc) {
-          char* const ns = slot_of(c + 1);
+        block_barrier();  // tile c complete for every wave; slot of the previous tile free
+        if (i + 1 < nsteps) {
+          char* const ns = slot_of(c + dir);
           if (kbn >= 0 && kbn + ROWS - 1 <= last) {
             // buffer loads into LDS: scalar descriptors for the two tiles and
             // the 32-bit per-lane offsets as they are (no 64-bit address)
@@ -299,14 +316,14 @@ void prefill_mfma_kernel(PrefillParams p) {
             for (int k = 0; k < NI; ++k)
               dma16_buf(G::instr_is_v(wid, k) ? rv : rk, voff[k], G::dst(ns, wid, k));
           } else {
-            issue(c + 1);
+            issue(c + dir);
           }
         }
-        kbn += kChunk;
+        kbn += dir * kChunk;
         kn += kstep;
         vn += vstep;
         if constexpr (kV1Ring)
-          if (c + 1 == p.nc) dma_tile(std::integral_constant<int, 2>{}, v1slot, kbs, p.k2, p.v1);  // v1 rows
+          if (i + 1 == nsteps) dma_tile(std::integral_constant<int, 2>{}, v1s, kbs, p.k2, p.v1);  // v1 rows
         // Unconditional: a wave without valid keys in this step gets an empty
         // key range (every p = 0, an exact no-op).  A branch here would give
         // the accumulators two incoming values at the loop latch, which the
@@ -319,7 +336,7 @@ void prefill_mfma_kernel(PrefillParams p) {
                                                                active ? min(t - kfirst, kChunk - 1) : -1);
       }
       if constexpr (kV1Ring)
-        if (c0 >= p.nc) dma_tile(std::integral_constant<int, 2>{}, v1slot, kbs, p.k2, p.v1);
+        if (nsteps <= 0) dma_tile(std::integral_constant<int, 2>{}, v1s, kbs, p.k2, p.v1);
     }
     wait_vmcnt<0>();  // this wave's part of the v1 rows
     block_barrier();  // ring reads done; v1 rows complete
@@ -343,7 +360,7 @@ void prefill_mfma_kernel(PrefillParams p) {
     // hoisted and kept live (or spilled) through the key loop
     const int lf = fresh_lane();
     const int hf = lf >> 5, g16 = (lf >> 4) & 1, i16 = lf & 15;
-    const uint32_t v1p = lds_addr(v1slot + G::VOFF + (qo + 7 - 4 * hf - (i16 >> 2)) * G::RSV + 32 * g16 +
+    const uint32_t v1p = lds_addr(v1s + G::VOFF + (qo + 7 - 4 * hf - (i16 >> 2)) * G::RSV + 32 * g16 +
                                   8 * (i16 & 3));
     static_for<0, DV / 32>([&](auto dd) {
       constexpr int db = decltype(dd)::value;
