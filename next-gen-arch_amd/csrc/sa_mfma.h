@@ -257,9 +257,10 @@ __device__ __forceinline__ void pack_bf16_split(float p0, float p1, uint32_t& hi
 // joint softmax of the reference has one max per query and head, and every
 // row of the wave belongs to the same query and head), moved lazily, by a
 // two-level rule.  The chunk loop (chunk) computes probabilities against the
-// current reference without a chunk maximum; only when some row's chunk sum
-// passes kLazyBound = 2^24 (a first valid chunk, a score far above the
-// reference, an overflow) does it take the chunk maxima and call rescale,
+// current reference without a chunk maximum, except in the wave's first chunk
+// with a valid key (the reference is still kMInit there); only when some
+// row's chunk sum passes kLazyBound = 2^24 (a score far above the reference,
+// an overflow) does it take the chunk maxima and call rescale,
 // which moves the reference only when a row's maximum exceeds it by more than
 // 8 in the log2 domain (a factor 2^8), and then to the largest such maximum,
 // and recomputes the chunk.  The pipelined step (step) calls rescale with
@@ -545,12 +546,23 @@ struct RowBlock {
         else pk[r >> 1] = pack_bf16(p0, p1);
       }
     };
-    probs();
-    if (__builtin_amdgcn_ballot_w64(!(zs <= kLazyBound)) != 0ull) {
+    auto move_reference = [&]() {
       float rmax = -INFINITY;
 #pragma unroll
       for (int r = 0; r < 16; ++r) rmax = fmaxf(rmax, s[r]);
       rescale(pair_max(rmax) * sl2);
+    };
+    // Until the wave's first chunk with a valid key the reference is kMInit,
+    // against which every valid probability overflows: at widths of 256 (few
+    // chunks per pass, two passes per query at C4) take that chunk's maxima
+    // before the probabilities instead of after -- the same reference, one
+    // pass of exponentials instead of two (C4 -2 %; at widths up to 128 the
+    // per-chunk test cost more than it saved: NS +0.6 %).
+    if constexpr (DK >= 256 || DV >= 256)
+      if (m == kMInit) move_reference();
+    probs();
+    if (__builtin_amdgcn_ballot_w64(!(zs <= kLazyBound)) != 0ull) {
+      move_reference();
       probs();
     }
     z += zs;
@@ -676,10 +688,12 @@ struct RowBlock {
     const bool grow = cand > m + 8.0f;
     if (__builtin_amdgcn_ballot_w64(grow) != 0ull) {
       const float mn = fmaxf(m, uniform_f(wave_max(cand)));
-      const float alpha = fast_exp2(m - mn);
+      if (m != kMInit) {  // before the first move nothing has been accumulated: o = 0, z = 0
+        const float alpha = fast_exp2(m - mn);
 #pragma unroll
-      for (int i = 0; i < DV / 32; ++i) o[i] *= alpha;
-      z *= alpha;
+        for (int i = 0; i < DV / 32; ++i) o[i] *= alpha;
+        z *= alpha;
+      }
       m = mn;
       mb = valid ? m : INFINITY;
     }
