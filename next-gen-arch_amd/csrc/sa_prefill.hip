@@ -102,7 +102,7 @@ void prefill_mfma_kernel(PrefillParams p) {
   // bf16 widths up to 128: the A-row inputs are staged in LDS (k1 rows in the
   // K region, q rows in the V region of a free ring slot; at 256 the staged
   // form costs the kernel register spills)
-  constexpr bool kStageA = !kV1Ring;
+  constexpr bool kStageA = !F32 && DK <= 256;
 
   const int tid = tid_x();
   const int lane = tid & 63;
@@ -257,9 +257,12 @@ void prefill_mfma_kernel(PrefillParams p) {
       dma_tile(std::integral_constant<int, 1>{}, kslot, kbs, (const bf16*)p.k1, p.v1);
       if (wid == 0) {
         constexpr int kQI = (NQ * NH * 2 * DK + 1023) / 1024;
+        // addresses from a fresh lane id: the same in every pass, they were
+        // hoisted out of the pass loop and spilled at widths of 256
+        const int lq = fresh_lane();
 #pragma unroll
         for (int k = 0; k < kQI; ++k) {
-          const int b = 1024 * k + 16 * lane;
+          const int b = 1024 * k + 16 * lq;
           const int pr = min(b / (2 * DK), NQ * NH - 1), seg = (b % (2 * DK)) / 16;  // pair (query, head)
           const int tq = min(t0 + pr / NH, last), hq = g * p.group + hs * NH + pr % NH;
           dma16((const bf16*)p.q + (int64_t)tq * p.q_st + (int64_t)hq * p.q_sh + 8 * seg, qslot + b);
