@@ -482,7 +482,7 @@ struct RowBlock {
   // for right after the MFMA before it).
   template <int RSK, int RSV, int PF = 1>
   __device__ __forceinline__ void chunk(const char* ktile, const char* vtile, int row0, int lane, float sl2,
-                                        int key_lo, int key_hi) {
+                                        int key_lo, int key_hi, bool first = false) {
     const int n = lane & 31, half = lane >> 5;
     floatx16 s = floatx16{};
     {
@@ -553,13 +553,11 @@ struct RowBlock {
       rescale(pair_max(rmax) * sl2);
     };
     // Until the wave's first chunk with a valid key the reference is kMInit,
-    // against which every valid probability overflows: at widths of 256 (few
-    // chunks per pass, two passes per query at C4) take that chunk's maxima
-    // before the probabilities instead of after -- the same reference, one
-    // pass of exponentials instead of two (C4 -2 %; at widths up to 128 the
-    // per-chunk test cost more than it saved: NS +0.6 %).
-    if constexpr (DK >= 256 || DV >= 256)
-      if (m == kMInit) move_reference();
+    // against which every valid probability overflows: in that chunk (`first`,
+    // a uniform flag from the caller's chunk index) take the maxima before the
+    // probabilities instead of after -- the same reference, one pass of
+    // exponentials instead of two.
+    if (first) move_reference();
     probs();
     if (__builtin_amdgcn_ballot_w64(!(zs <= kLazyBound)) != 0ull) {
       move_reference();

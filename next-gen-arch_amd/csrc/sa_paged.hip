@@ -339,9 +339,10 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 || NW < 4 ? 1 : 2)) void paged_m
           // unconditional (see the prefill kernel): idle waves get an empty key range
           const int kfirst = kstart + kChunk * c;
           const char* slot = lds + (c % R) * SLOT;
+          // the split's first chunk holds a valid key of the token
           rb.template chunk<G::RSK, G::RSV>(slot, slot + G::VOFF, 0, lane, p.sl2,
                                             task_ok ? max(lo2 - kfirst, 0) : kChunk,
-                                            task_ok ? min(pos - kfirst, kChunk - 1) : -1);
+                                            task_ok ? min(pos - kfirst, kChunk - 1) : -1, task_ok && c == cbeg);
         }
       }
       block_barrier();  // tile and row-offset reads of this segment done

@@ -332,11 +332,17 @@ void prefill_mfma_kernel(PrefillParams p) {
         // the accumulators two incoming values at the loop latch, which the
         // register allocator resolves by keeping a second copy of all of O.
         const bool active = qvalid && c >= cfirst;
+        // the pass's first chunk with a valid key for this wave: cfirst when
+        // ascending, the last chunk (it holds key t) when descending.  Widths
+        // of 256 only (C4 -0.9 %): over 16 chunks at widths up to 128 the
+        // per-chunk test cost as much as it saved (NS +0.2 %, C3 +0.9 %), and
+        // the first chunk there computes its probabilities twice instead.
+        const bool first = (DK >= 256 || DV >= 256) && qvalid && c == (rev ? p.nc - 1 : cfirst);
         const int kfirst = t - p.wl + 1 + kChunk * c;  // key of this wave's chunk row 0
         const char* slot = slot_of(c);
         rb.template chunk<G::RSK, G::RSV, (DK >= 512 ? kPrefillChunkPFWide : kPrefillChunkPF)>(slot, slot + G::VOFF, qo, lane, p.sl2,
                                                                active ? max(lo2 - kfirst, 0) : kChunk,
-                                                               active ? min(t - kfirst, kChunk - 1) : -1);
+                                                               active ? min(t - kfirst, kChunk - 1) : -1, first);
       }
       if constexpr (kV1Ring)
         if (nsteps <= 0) dma_tile(std::integral_constant<int, 2>{}, v1s, kbs, p.k2, p.v1);
