@@ -373,32 +373,6 @@ struct RowBlock {
                                          int half, bool q_neg) {
     make_a(load_a(q, k1, half), valid, q_neg);
   }
-  // The same from global memory in groups of four fragments (wide score
-  // rows: loading all 2 DK/16 input fragments at once would hold DK/2 VGPRs);
-  // lanes outside the window pass a row of zeros.
-  __device__ __forceinline__ void form_a_grouped(const bf16* __restrict__ q, const bf16* __restrict__ k1, int half,
-                                                 bool q_neg) {
-    constexpr int GRP = 4;
-    const uint32_t sgn = q_neg ? 0x80008000u : 0u;
-#pragma unroll
-    for (int t0 = 0; t0 < DK / 16; t0 += GRP) {
-      bf16x8 qv[GRP], kv[GRP];
-#pragma unroll
-      for (int u = 0; u < GRP; ++u) {
-        const int d0 = 16 * (t0 + u) + 8 * half;
-        qv[u] = load_global<bf16x8>(q + d0);
-        kv[u] = load_global<bf16x8>(k1 + d0);
-      }
-#pragma unroll
-      for (int u = 0; u < GRP; ++u) {
-        const u32x4 qw = __builtin_bit_cast(u32x4, qv[u]), kw = __builtin_bit_cast(u32x4, kv[u]);
-        u32x4 r;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = mul_pair(qw[e], kw[e], sgn, 0xffffffffu);
-        a[t0 + u] = __builtin_bit_cast(bf16x8, r);
-      }
-    }
-  }
   // HL: a_j = q ⊙ k1_j with an fp32 query, split into hi + lo terms.
   // K1 = bf16 (paged caches) or float (fp32 prefill)
   template <typename K1>

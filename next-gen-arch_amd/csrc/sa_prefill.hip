@@ -35,9 +35,6 @@
 
 namespace sa {
 
-// A k1 row of zeros (score widths up to 512) for A rows outside the short window.
-static __device__ __align__(16) const uint32_t kZeroRow[256] = {};
-
 struct PrefillParams {
   const void* q;   // bf16, or fp32 (F32 kernels)
   const void* k1;  // bf16, or fp32 (F32 kernels)
@@ -99,10 +96,10 @@ void prefill_mfma_kernel(PrefillParams p) {
   // merge): placed so that their V region is the area after the ring (widths
   // up to 128; otherwise a ring slot chosen per pass, below).
   char* const v1slot = lds + R * G::SLOT - G::VOFF;
-  // bf16 widths up to 128: the A-row inputs are staged in LDS (k1 rows in the
-  // K region, q rows in the V region of a free ring slot; at 256 the staged
-  // form costs the kernel register spills)
-  constexpr bool kStageA = !F32 && DK <= 256;
+  // bf16: the A-row inputs are staged in LDS (k1 rows in the K region, q rows
+  // in the V region of a free ring slot) at every width; fp32 inputs form A
+  // from global memory
+  constexpr bool kStageA = !F32;
 
   const int tid = tid_x();
   const int lane = tid & 63;
@@ -245,7 +242,7 @@ void prefill_mfma_kernel(PrefillParams p) {
       // waits cover them)
       dma_tile(std::integral_constant<int, 2>{}, v1slot, kbs, p.k2, p.v1);
     }
-    // bf16 widths up to 128: the block's k1 rows (rows kbs.., the K region of the ring slot
+    // bf16: the block's k1 rows (rows kbs.., the K region of the ring slot
     // that tile c0+1 fills only after the key loop's first barrier) and its q
     // rows (that slot's V region) are staged once per block by DMA ahead of
     // the first tile, and the A rows are formed from LDS while the tile
@@ -279,20 +276,12 @@ void prefill_mfma_kernel(PrefillParams p) {
       // the window are masked
       rb.form_a_lds(kslot + (qo + 31 - n) * G::RSK, qslot + wid * 2 * DK, row_ok, half, p.q_neg != 0);
     } else {
+      // fp32 inputs: A formed in fp32 from the rows in global memory and split
+      // into hi/lo terms
+      static_assert(F32, "bf16 A-row inputs are staged");
       const int64_t qoff = (int64_t)min(t, last) * p.q_st + (int64_t)h * p.q_sh;
       const int64_t k1off = (int64_t)jc * p.k1_st + (int64_t)g * p.k1_sh;
-      if constexpr (F32)
-        rb.form_a_f32((const float*)p.q + qoff, (const float*)p.k1 + k1off, row_ok, half, p.q_neg != 0);
-      else {
-        // lanes outside the window read a row of zeros (A = 0 without a mask)
-        const bf16* k1row = row_ok ? (const bf16*)p.k1 + k1off : (const bf16*)kZeroRow;
-        if constexpr (DK >= 512) {
-          rb.form_a_grouped((const bf16*)p.q + qoff, k1row, half, p.q_neg != 0);
-        } else {
-          const auto ain = RB::load_a((const bf16*)p.q + qoff, k1row, half);
-          rb.make_a(ain, true, p.q_neg != 0);
-        }
-      }
+      rb.form_a_f32((const float*)p.q + qoff, (const float*)p.k1 + k1off, row_ok, half, p.q_neg != 0);
     }
     rb.reset(row_ok);
     {
