@@ -412,6 +412,74 @@ struct RowBlock {
       al[t] = l;
     }
   }
+  // The wave's q row (DK bf16 at qrow, in LDS) widened to DK fp32 values at
+  // qf (LDS), negated when q_neg; each lane widens DK / 64 of them.  A wave's
+  // LDS accesses execute in order, so its lanes may read qf right after (no
+  // barrier), and form_a_qf then multiplies without unpacking q per lane.
+  __device__ static __forceinline__ void widen_q(const char* qrow, char* qf, int lane, bool q_neg) {
+    constexpr int W = DK >= 128 ? DK / 128 : 1;  // packed words per lane
+    constexpr int LANES = DK / 2 / W;            // lanes with words (all but DK = 64)
+    static_assert(W == 1 || W == 2 || W == 4, "widths 64 .. 512");
+    const uint32_t sgn = q_neg ? 0x80000000u : 0u;
+    if (LANES == 64 || lane < LANES) {
+      uint32_t w[W];
+      if constexpr (W == 4) {
+        const u32x4 x = *(const u32x4*)(qrow + 16 * lane);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = x[e];
+      } else if constexpr (W == 2) {
+        const uint2 x = *(const uint2*)(qrow + 8 * lane);
+        w[0] = x.x, w[1] = x.y;
+      } else {
+        w[0] = *(const uint32_t*)(qrow + 4 * lane);
+      }
+      float f[2 * W];
+#pragma unroll
+      for (int e = 0; e < W; ++e) {
+        f[2 * e] = __uint_as_float((w[e] << 16) ^ sgn);
+        f[2 * e + 1] = __uint_as_float((w[e] & 0xffff0000u) ^ sgn);
+      }
+      float* dst = (float*)qf + 2 * W * lane;
+      if constexpr (W == 1) {
+        *(floatx2*)dst = floatx2{f[0], f[1]};
+      } else {
+#pragma unroll
+        for (int e = 0; e < W / 2; ++e) *(floatx4*)(dst + 4 * e) = floatx4{f[4 * e], f[4 * e + 1], f[4 * e + 2], f[4 * e + 3]};
+      }
+    }
+  }
+  // A rows from the lane's staged k1 row (krow, DK bf16) and the wave's
+  // widened q row (qf, DK fp32 with the sign of q_neg applied): the products
+  // of the same operands as form_a_lds, so the same bits.  Fragments are read
+  // in groups (bounded register footprint).
+  __device__ __forceinline__ void form_a_qf(const char* krow, const char* qf, bool valid, int half) {
+    constexpr int GRP = DK / 16 < 4 ? DK / 16 : 4;
+    const uint32_t keep = valid ? 0xffffffffu : 0u;
+#pragma unroll
+    for (int t0 = 0; t0 < DK / 16; t0 += GRP) {
+      floatx4 qv[GRP][2];
+      u32x4 kv[GRP];
+#pragma unroll
+      for (int u = 0; u < GRP; ++u) {
+        const char* qp = qf + 4 * (16 * (t0 + u) + 8 * half);
+        qv[u][0] = *(const floatx4*)qp;
+        qv[u][1] = *(const floatx4*)(qp + 16);
+        kv[u] = *(const u32x4*)(krow + 32 * (t0 + u) + 16 * half);
+      }
+#pragma unroll
+      for (int u = 0; u < GRP; ++u) {
+        u32x4 r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = qv[u][e >> 1][2 * (e & 1)] * __uint_as_float(kv[u][e] << 16);
+          const float hi = qv[u][e >> 1][2 * (e & 1) + 1] * __uint_as_float(kv[u][e] & 0xffff0000u);
+          r[e] = pack_bf16(lo, hi) & keep;
+        }
+        a[t0 + u] = __builtin_bit_cast(bf16x8, r);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
   // The same from rows staged in LDS: krow = the lane's k1 row, qrow = the
   // wave's q row (both DK contiguous bf16).
   // Fragments are read in groups of 4 (bounded register footprint).

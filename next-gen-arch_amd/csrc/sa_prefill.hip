@@ -272,9 +272,13 @@ void prefill_mfma_kernel(PrefillParams p) {
       if (resident) wait_vmcnt<0>();
       else wait_vmcnt<G::NI>();
       block_barrier();
-      // lane n's k1 row j = t - 32r - n is slot row qo + 31 - n; rows outside
-      // the window are masked
-      rb.form_a_lds(kslot + (qo + 31 - n) * G::RSK, qslot + wid * 2 * DK, row_ok, half, p.q_neg != 0);
+      // the wave's q row widened to fp32 after the staged rows (same slot
+      // region), then lane n's k1 row j = t - 32r - n is slot row qo + 31 - n;
+      // rows outside the window are masked
+      char* const qf = qslot + NQ * NH * 2 * DK + wid * 4 * DK;
+      static_assert(NQ * NH * 6 * DK <= G::SLOT - G::VOFF, "staged and widened q rows fit the V region");
+      RB::widen_q(qslot + wid * 2 * DK, qf, fresh_lane(), p.q_neg != 0);
+      rb.form_a_qf(kslot + (qo + 31 - n) * G::RSK, qf, row_ok, half);
     } else {
       // fp32 inputs: A formed in fp32 from the rows in global memory and split
       // into hi/lo terms
