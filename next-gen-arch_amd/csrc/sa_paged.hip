@@ -142,7 +142,7 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 || NW < 4 ? 1 : 2)) void paged_m
   // segment's third tile fills only after the key loop's first barrier.
   constexpr int QB = (QF32 ? 4 : 2) * D;         // bytes of one q row
   int64_t* const soffs = roff + kPosCache;       // [32] short-row offsets
-  char* const qslot = (char*)(soffs + 32);       // [NW] q rows, QB bytes each
+  char* const qslot = (char*)(soffs + 32);       // [NW] q rows, QB bytes each (bf16 staged: then [NW] fp32 rows)
   constexpr bool kStage = D <= 128 && P >= 2 && P * NI < 64 && !MULTI;  // the wait below counts P tiles' DMAs
   const bool stage = kStage && p.nr == 1;        // uniform
   // Lookups are branch-free (clamped indices) so that every load of a batch
@@ -270,7 +270,12 @@ __global__ __launch_bounds__(64 * NW, (D >= 256 || NW < 4 ? 1 : 2)) void paged_m
           if constexpr (QF32)
             rb.form_a_f32((const float*)(qslot + wid * QB), (const bf16*)(sslot + n * G::RSK), row_ok, half,
                           p.q_neg != 0);
-          else rb.form_a_lds(sslot + n * G::RSK, qslot + wid * QB, row_ok, half, p.q_neg != 0);
+          else {
+            // the wave's q row widened to fp32 (after the NW staged rows)
+            char* const qf = qslot + NW * QB + wid * 4 * D;
+            RB::widen_q(qslot + wid * QB, qf, fresh_lane(), p.q_neg != 0);
+            rb.form_a_qf(sslot + n * G::RSK, qf, row_ok, half);
+          }
           if constexpr (kV1Regs) {
             const char* v1s = sslot + G::VOFF + n * G::RSV;
 #pragma unroll
@@ -546,12 +551,15 @@ static hipError_t launch_paged_mfma_t(PagedParams p, hipStream_t stream) {
   constexpr int P = D >= 256 ? 2 : kPagedDepth;
   // ring, row offsets, the short-row offsets and the staged q rows; the
   // epilogue's per-wave reduction area overlays the ring
-  const size_t lds_ring = (size_t)(P + 1) * FwdGeom<D, D, kChunk, NW>::SLOT + kPosCache * sizeof(int64_t) +
-                          32 * sizeof(int64_t) + (size_t)(NW * (QF32 ? 4 : 2) * D + 1023) / 1024 * 1024;
-  const size_t lds_red = (size_t)NW * 64 * 36 * sizeof(float);
-  const size_t lds = lds_ring > lds_red ? lds_ring : lds_red;
   // a split holds at most ceil(nc / splits) chunks
   const bool multi = (p.nc + p.splits - 1) / p.splits > kSegChunks;
+  // staged bf16 q rows (D <= 128, one segment) are also widened to fp32
+  const bool widen = !QF32 && D <= 128 && !multi;
+  const size_t qbytes = (size_t)NW * (QF32 ? 4 : 2) * D + (widen ? (size_t)NW * 4 * D : 0);
+  const size_t lds_ring = (size_t)(P + 1) * FwdGeom<D, D, kChunk, NW>::SLOT + kPosCache * sizeof(int64_t) +
+                          32 * sizeof(int64_t) + (qbytes + 1023) / 1024 * 1024;
+  const size_t lds_red = (size_t)NW * 64 * 36 * sizeof(float);
+  const size_t lds = lds_ring > lds_red ? lds_ring : lds_red;
   auto kern = multi ? paged_mfma_kernel<D, NW, P, true, QF32> : paged_mfma_kernel<D, NW, P, false, QF32>;
   hipError_t e = set_lds_limit((const void*)kern, lds);
   if (e != hipSuccess) return e;
