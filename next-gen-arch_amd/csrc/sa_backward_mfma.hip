@@ -1170,6 +1170,8 @@ __global__ __launch_bounds__(256) void bwd_dk1_sum_kernel(BwdParams p, int qbloc
 // MODE 1: dK2 only, MODE 2: dV2 only (two launches).  Each holds one
 // accumulator set, and the dV2 launch neither the V2 fragments nor dP, so
 // both fit two waves per SIMD; the S recomputation is paid twice.
+// MODE 3 (fp32 inputs, which run one wave per SIMD either way): dK2 and dV2
+// in one launch from one S per step and one formation of the A / B rows.
 // PH (phased): twice the short-key rows of one launch run as two launches,
 // phase 1 (row groups 0 .. NR-1: rows j = t - 32 NR + 1 .. t) writing its fp32
 // sums to p.dkv2p and phase 2 (groups NR .. 2NR-1) starting from them and
@@ -1187,7 +1189,9 @@ __global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_
                                                                                            int nblocks, int phase,
                                                                                            int splits) {
   static_assert(!F32 || (DK == DV && DK <= 128 && NR == 1 && !PH), "fp32 inputs: equal widths up to 128, one group");
-  constexpr bool kDK = MODE == 1, kDV = MODE == 2;
+  constexpr bool kBoth = MODE == 3;  // dK2 and dV2 (fp32)
+  static_assert(!kBoth || F32, "both gradients in one launch: fp32 inputs");
+  constexpr bool kDK = MODE == 1 || kBoth, kDV = MODE == 2 || kBoth;
   constexpr int EW = F32 ? 2 : 1;  // bf16 units per element of an LDS row
   constexpr int kKvRing = 64 * NR;  // k1 / v1 ring rows (a power of two)
   constexpr int KB = 32 * NWK;    // keys per workgroup
@@ -1195,8 +1199,8 @@ __global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_
   // LDS reads in flight ahead of their MFMA: with two waves per SIMD, one
   // read ahead leaves each step's three MFMA chains waiting on LDS latency
   constexpr int kPF = DK >= 256 ? kDkv2PFWide : kDkv2PF;
-  static_assert(kDK || kDV, "one output per launch");
-  constexpr int XW = kDK ? DK : DV;        // width of the gradient accumulated
+  static_assert(kDK || kDV, "an output per launch");
+  constexpr int XW = kDK ? DK : DV;        // width of the gradient accumulated in acc (dK2 when both)
   using OPK = BwdOps<DK>;
   using OPV = BwdOps<DV>;
   // A / B tile row strides (padded: row and transposing reads)
@@ -1255,6 +1259,9 @@ __global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_
   floatx16 acc[XW / 32];  // dK2^T or dV2^T
 #pragma unroll
   for (int i = 0; i < XW / 32; ++i) acc[i] = floatx16{};
+  floatx16 accv[kBoth ? DV / 32 : 1];  // dV2^T (both gradients)
+#pragma unroll
+  for (int i = 0; i < (kBoth ? DV / 32 : 1); ++i) accv[i] = floatx16{};
   // fp32 sums of the first row group (phases 1 and 2): [tokens][hk][DK] for
   // dK2, then [tokens][hk][DV] for dV2, each lane's values at its d
   auto part_row = [&]() {
@@ -1305,8 +1312,12 @@ __global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_
           *(floatx4*)(part + 32 * db + 8 * q4 + 4 * half) = x;
         }
     } else if (F32) {
-      float* orow = kDK ? (float*)p.dk2 + (int64_t)kw * p.dk_st + (int64_t)g * p.dk_sh
-                        : (float*)p.dv2 + (int64_t)kw * p.dv_st + (int64_t)g * p.dv_sh;
+      // key and half from a fresh lane id: row addresses formed here, not
+      // held (or spilled) through the step loop
+      const int lf = fresh_lane();
+      const int kwf = k0 + 32 * wid + (lf & 31), hf = lf >> 5;
+      float* orow = kDK ? (float*)p.dk2 + (int64_t)kwf * p.dk_st + (int64_t)g * p.dk_sh
+                        : (float*)p.dv2 + (int64_t)kwf * p.dv_st + (int64_t)g * p.dv_sh;
 #pragma unroll
       for (int db = 0; db < XW / 32; ++db)
 #pragma unroll
@@ -1314,8 +1325,20 @@ __global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_
           floatx4 a;
 #pragma unroll
           for (int e = 0; e < 4; ++e) a[e] = acc[db][4 * q4 + e];
-          *(floatx4*)(orow + 32 * db + 8 * q4 + 4 * half) = a;
+          *(floatx4*)(orow + 32 * db + 8 * q4 + 4 * hf) = a;
         }
+      if constexpr (kBoth) {
+        float* vrow = (float*)p.dv2 + (int64_t)kwf * p.dv_st + (int64_t)g * p.dv_sh;
+#pragma unroll
+        for (int db = 0; db < DV / 32; ++db)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            floatx4 a;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a[e] = accv[db][4 * q4 + e];
+            *(floatx4*)(vrow + 32 * db + 8 * q4 + 4 * hf) = a;
+          }
+      }
     } else {
       bf16* orow = kDK ? (bf16*)p.dk2 + (int64_t)kw * p.dk_st + (int64_t)g * p.dk_sh
                        : (bf16*)p.dv2 + (int64_t)kw * p.dv_st + (int64_t)g * p.dv_sh;
@@ -1641,8 +1664,8 @@ __global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_
     // dK2^T += A_t^T · dS^T, or dV2^T += B_t^T · P^T
     auto accumulate = [&](const floatx16& s_, const floatx16& dp_, int ilo_r, const char* At_r, const char* Bt_r) {
       if constexpr (F32) {
-        // dS (dK2 launch) or P (dV2 launch) in fp32, as hi/lo B operands
-        float x[16];
+        // dS (dK2) and / or P (dV2) in fp32, as hi/lo B operands
+        float x[16], pv[kBoth ? 16 : 1];
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int ie = 8 * (e >> 2) + 4 * half + (e & 3);
@@ -1650,11 +1673,16 @@ __global__ __launch_bounds__(64 * NWK, (DK > 128 || F32) ? 1 : 2) void bwd_dkv2_
           const float pe = ok ? fast_exp2(fmaf(s_[e], sl2s, -lse2)) : 0.f;
           if constexpr (kDK) x[e] = pe * fmaf(dp_[e], dpm, dsm);
           else x[e] = pe;
+          if constexpr (kBoth) pv[e] = pe;
         }
         bf16x8 b0, b1, l0, l1;
         OPK::pack_c_hl(x, b0, b1, l0, l1);
         if constexpr (kDK) OPK::template tr_acc_hl<RSA>(acc, At_r, 0, lane, b0, b1, l0, l1);
         else OPV::template tr_acc_hl<RSB>(acc, Bt_r, 0, lane, b0, b1, l0, l1);
+        if constexpr (kBoth) {
+          OPK::pack_c_hl(pv, b0, b1, l0, l1);
+          OPV::template tr_acc_hl<RSB>(accv, Bt_r, 0, lane, b0, b1, l0, l1);
+        }
         return;
       }
       uint32_t pk[8];  // bf16(dS) (dK2 launch) or bf16(P) (dV2 launch)
@@ -1736,9 +1764,13 @@ hipError_t launch_dkv2_t(const BwdParams& p, int splits, hipStream_t stream) {
   const bool two = PH && p.ws > 32 * NR;
   if (two || F32 || !p.dkv2s) splits = 1;
   const int nblocks = (p.tokens + 32 * NWK - 1) / (32 * NWK) * p.hk * splits;
-  for (int mode = 1; mode <= 2; ++mode) {
-    auto kern = mode == 1 ? bwd_dkv2_mfma_kernel<DK, DV, 1, NWK, NR, PH, F32>
-                          : bwd_dkv2_mfma_kernel<DK, DV, 2, NWK, NR, PH, F32>;
+  // fp32: one launch for both gradients (mode 3); bf16: dK2, then dV2
+  for (int mode = F32 ? 3 : 1; mode <= (F32 ? 3 : 2); ++mode) {
+    auto kern = [&]() {
+      if constexpr (F32) return bwd_dkv2_mfma_kernel<DK, DV, 3, NWK, NR, PH, true>;
+      else return mode == 1 ? bwd_dkv2_mfma_kernel<DK, DV, 1, NWK, NR, PH, false>
+                            : bwd_dkv2_mfma_kernel<DK, DV, 2, NWK, NR, PH, false>;
+    }();
     hipError_t e = set_lds_limit((const void*)kern, lds);
     if (e != hipSuccess) return e;
     for (int phase = two ? 1 : 0; phase <= (two ? 2 : 0); ++phase) {
