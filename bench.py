@@ -367,7 +367,10 @@ def backward_leg(args, fwd_ms, workload=None, cfg=None):
         "bwd_frac_of_peak": flops / (bwd_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
         "bwd_valid_pair_flops": valid, "bwd_valid_pair_tflops": valid / (bwd_ms * 1e-3) / 1e12,
         "dtype": str(cfg.dtype).replace("torch.", ""),
-        "kernels": "bwd_dq_mfma_kernel, bwd_dkv1_mfma_kernel, bwd_dkv2_mfma_kernel (+ bwd_delta_kernel)",
+        "kernels": ("bwd_dq_mfma_kernel (dq, dk1 and dv1 partials), bwd_dk1_sum_kernel, bwd_dkv2_mfma_kernel "
+                    "(dk2 and dv2 in one launch) (+ split_hilo_kernel, bwd_delta_kernel)"
+                    if cfg.dtype == torch.float32 else
+                    "bwd_dq_mfma_kernel, bwd_dkv1_mfma_kernel, bwd_dkv2_mfma_kernel (+ bwd_delta_kernel)"),
     }
 
 

@@ -35,6 +35,10 @@ struct BwdParams {
   // short-key rows of Σ dA_{t,j} ⊙ q_{t,h}, fp32 [hk * hsub][qblocks][nr]
   // [31 + NQ][D], summed by bwd_dk1_sum_kernel; null: the separate dk1 pass
   float* dk1p;
+  // fp32 inputs with dk1p: dv1 from the dq pass as well, the same rows of
+  // Σ O''_{t,j} ⊙ dout_{t,h} (O''_{t,j} = Σ_k P_{t,j,k} v2_k), [hk * hsub]
+  // [qblocks][nr][31 + NQ][DV]; null: the dk1 / dv1 pass computes dv1
+  float* dv1p;
   // Short windows of 65-128 keys (33-64 at score width 256): the dk2 / dv2
   // passes run as two launches and carry the first one's fp32 sums here,
   // [tokens][hk][D] then [tokens][hk][DV]; null: the portable dk2 / dv2 pass
@@ -67,6 +71,8 @@ hipError_t launch_bwd_dkv2_mfma(const BwdParams& p, hipStream_t stream);
 bool bwd_dk1_fused_ok(const BwdParams& p);
 // dk1 = the fixed-order sum of the dq pass's partials (p.dk1p)
 hipError_t launch_bwd_dk1_sum(const BwdParams& p, hipStream_t stream);
+// dv1 = the same sum of the dq pass's dv1 partials (p.dv1p, fp32 inputs)
+hipError_t launch_bwd_dv1_sum(const BwdParams& p, hipStream_t stream);
 
 // MFMA dk2 / dv2 pass: waves per workgroup (32 long keys each) and walk
 // splits (pieces of each workgroup's walk over the queries, for shapes whose

@@ -571,6 +571,20 @@ static size_t dk1_partial_bytes(const sa_prefill_bwd_args* a) {
   const size_t bytes = (qblocks * heads * nr * (31 + nq) * f.head_dim * sizeof(float) + 255) & ~(size_t)255;
   return bytes <= kDk1PartialCap ? bytes : 0;
 }
+// fp32 inputs with dk1 from the dq pass: dv1 from it as well, the same rows
+// at the value width; both together within kDk1PartialCap (else the dk1 / dv1
+// pass computes dv1)
+static size_t dv1_partial_bytes(const sa_prefill_bwd_args* a) {
+  const sa_prefill_args& f = a->fwd;
+  const size_t k = dk1_partial_bytes(a);
+  if (f.dtype != SA_DTYPE_F32 || !k) return 0;
+  const int nq = dq_queries_per_block(f.heads_q / f.heads_kv);
+  const size_t qblocks = ((size_t)f.total_tokens + nq - 1) / nq;
+  const size_t heads = (size_t)f.heads_q / (4 / nq);
+  const size_t nr = ((size_t)f.short_window + 31) / 32;
+  const size_t v = (qblocks * heads * nr * (31 + nq) * f.value_dim * sizeof(float) + 255) & ~(size_t)255;
+  return k + v <= kDk1PartialCap ? v : 0;
+}
 // Short windows past what one MFMA dk2 / dv2 launch holds (64 keys at widths
 // <= 128, 32 at score width 256) and up to twice that: the first launch's fp32
 // dk2 and dv2 sums.
@@ -601,7 +615,7 @@ static size_t dkv2_split_bytes(const sa_prefill_bwd_args* a) {
 }
 size_t prefill_bwd_workspace_bytes(const sa_prefill_bwd_args* a) {
   return 2 * bwd_row_bytes(a) + dk1_partial_bytes(a) + dkv2_partial_bytes(a) + 2 * f32_split_bytes(a) +
-         dkv2_split_bytes(a);
+         dkv2_split_bytes(a) + dv1_partial_bytes(a);
 }
 
 template <typename T>
@@ -637,10 +651,14 @@ static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
     e = launch_bwd_dk1_sum(p, stream);
     if (e != hipSuccess) return e;
   }
-  e = launch_bwd_dkv1_mfma(p, stream);
-  if (e == hipErrorNotSupported) {
-    hipLaunchKernelGGL(bwd_dkv1_kernel<T>, ks[1].grid, dim3(kBwdThreads), ks[1].lds, stream, p);
-    e = hipGetLastError();
+  if (p.dv1p) {  // dv1 from the dq pass's partials as well: no dk1 / dv1 pass
+    e = launch_bwd_dv1_sum(p, stream);
+  } else {
+    e = launch_bwd_dkv1_mfma(p, stream);
+    if (e == hipErrorNotSupported) {
+      hipLaunchKernelGGL(bwd_dkv1_kernel<T>, ks[1].grid, dim3(kBwdThreads), ks[1].lds, stream, p);
+      e = hipGetLastError();
+    }
   }
   if (e != hipSuccess) return e;
   e = launch_bwd_dkv2_mfma(p, stream);
@@ -718,6 +736,9 @@ hipError_t launch_prefill_bwd(const sa_prefill_bwd_args* a, void* ws, hipStream_
     p.v2s = v2s;
   }
   if (dk1_partial_bytes(a) && bwd_dk1_fused_ok(p)) p.dk1p = (float*)((char*)ws + 2 * bwd_row_bytes(a));
+  if (dv1_partial_bytes(a) && p.dk1p)
+    p.dv1p = (float*)((char*)ws + 2 * bwd_row_bytes(a) + dk1_partial_bytes(a) + dkv2_partial_bytes(a) +
+                      2 * f32_split_bytes(a) + dkv2_split_bytes(a));
   if (dkv2_partial_bytes(a)) p.dkv2p = (float*)((char*)ws + 2 * bwd_row_bytes(a) + dk1_partial_bytes(a));
   if (dkv2_split_bytes(a))
     p.dkv2s = (float*)((char*)ws + 2 * bwd_row_bytes(a) + dk1_partial_bytes(a) + dkv2_partial_bytes(a) +

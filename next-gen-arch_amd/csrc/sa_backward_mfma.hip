@@ -279,10 +279,15 @@ struct BwdGeo {
 // (p.k2s, p.v2s), the short slot and the q / dout rows hold fp32 rows (the
 // same bytes as a hi/lo row), A and B are split from fp32 products, and every
 // product runs on three term pairs; dq (and dk1) in fp32.
-template <int DK, int DV, int NQ, int NH, int P, bool FUSE = false, bool F32 = false>
+// FV (fp32 inputs with FUSE; one wave per SIMD either way): the pass also
+// accumulates O''^T += V2^T · P^T per chunk and writes the block's dv1
+// partials, Σ O''_{t,j} ⊙ dout_{t,h} over the same rows as dk1's, so that no
+// dk1 / dv1 pass recomputes S.
+template <int DK, int DV, int NQ, int NH, int P, bool FUSE = false, bool F32 = false, bool FV = false>
 __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_dq_mfma_kernel(BwdParams p,
                                                                                             BwdGeo geo) {
   static_assert(NQ * NH == 4, "4 waves per block");
+  static_assert(!FV || (F32 && FUSE && DK == DV), "dv1 partials: fp32 inputs, with the dk1 partials");
   static_assert(!F32 || (DK == DV && DK <= 128), "fp32 inputs: equal widths up to 128");
   constexpr int NW = NQ * NH;
   constexpr int ROWS = kChunk + NQ - 1;
@@ -444,6 +449,9 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_d
     floatx16 dA[DK / 32];
 #pragma unroll
     for (int i = 0; i < DK / 32; ++i) dA[i] = floatx16{};
+    floatx16 dO[FV ? DV / 32 : 1];  // O''^T (dv1 partials)
+#pragma unroll
+    for (int i = 0; i < (FV ? DV / 32 : 1); ++i) dO[i] = floatx16{};
     for (int c = c0; c < geo.nc; ++c) {
       wait_tiles<NI, P>(min(P - 1, geo.nc - 1 - c));
       block_barrier();  // tile c complete for every wave; the slot of tile c-1 is free
@@ -463,17 +471,22 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_d
       }
       // register r holds chunk key 8*(r/4) + r%4 + 4*half of column j = this lane's row
       const int lo_h = klo - 4 * half, hi_h = khi - 4 * half;
-      float ds[16];
+      float ds[16], pv[FV ? 16 : 1];  // dS, and (FV) P
       if (klo <= 0 && khi >= kChunk - 1) {  // every key of the chunk valid (uniform test)
         // rows outside the window: exp2(s*c - inf) = 0 with no per-key test
 #pragma unroll
-        for (int e = 0; e < 16; ++e) ds[e] = fast_exp2(fmaf(s[e], sl2s, -lse2r)) * fmaf(dp[e], dpm, dsm);
+        for (int e = 0; e < 16; ++e) {
+          const float pr = fast_exp2(fmaf(s[e], sl2s, -lse2r));
+          if constexpr (FV) pv[e] = pr;
+          ds[e] = pr * fmaf(dp[e], dpm, dsm);
+        }
       } else {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int kr = 8 * (e >> 2) + (e & 3);
           const bool ok = row_ok && kr >= lo_h && kr <= hi_h;
           const float pr = ok ? fast_exp2(fmaf(s[e], sl2s, -lse2)) : 0.f;
+          if constexpr (FV) pv[e] = pr;
           ds[e] = pr * fmaf(dp[e], dpm, dsm);
         }
       }
@@ -482,6 +495,10 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_d
         bf16x8 pl0, pl1;
         OPK::pack_c_hl(ds, pb0, pb1, pl0, pl1);
         OPK::template tr_acc_hl<G::RSK>(dA, slot, qo, lane, pb0, pb1, pl0, pl1);  // dA^T += K2^T · dS^T
+        if constexpr (FV) {
+          OPK::pack_c_hl(pv, pb0, pb1, pl0, pl1);
+          OPV::template tr_acc_hl<G::RSV>(dO, slot + G::VOFF, qo, lane, pb0, pb1, pl0, pl1);  // O''^T += V2^T · P^T
+        }
       } else {
         OPK::pack_c(ds, pb0, pb1);
         OPK::template tr_acc<G::RSK, kPF, kOT>(dA, slot, qo, lane, pb0, pb1);  // dA^T += K2^T · dS^T (kOT: dA, lane = d)
@@ -590,7 +607,7 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_d
     block_barrier();  // every wave's short-slot (and `red`) reads done before the next pass (or exit) reuses the LDS
 
     if constexpr (FUSE) {
-      // dk1 partial: row n of wave (qo, hw) is short key j = t0 + qo - 32 r - n,
+      // dk1 (and, FV, dv1) partial: row n of wave (qo, hw) is short key j = t0 + qo - 32 r - n,
       // partial row jrow = qo + 31 - n.  Per 64-wide d half, each wave stages
       // its 32 rows x 64 d products (rows of 68 floats), then the block sums
       // every (jrow, 4 d) over its waves in wave order and writes it.
@@ -603,80 +620,84 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_d
       constexpr int kPart = NW * 32 * PRS;      // floats of one staged half
       constexpr int DHR = RING / (4 * kPart) >= 2 && DK / 64 >= 2 && DV == DK ? 2 : 1;
       static_assert((DK / 64) % DHR == 0 && DHR * 4 * kPart <= RING, "staged halves fit the ring region");
-      const char* qrow = qslot + wid * G::RSK;  // q row of this wave's (t, h)
-      float* const dst = p.dk1p + (((int64_t)hg * geo.qblocks + qb) * geo.nr + r) * (ROWS1 * DK);
+      // rows of Σ X_{t,j} ⊙ v_{t,h} (X = dA, v = q: dk1; X = O'', v = dout: dv1)
+      auto write_partials = [&](const floatx16 (&X)[DK / 32], const char* vrow, float* const dst) {
 #pragma unroll
-      for (int dr = 0; dr < DK / 64; dr += DHR) {
+        for (int dr = 0; dr < DK / 64; dr += DHR) {
 #pragma unroll
-        for (int dh = dr; dh < dr + DHR; ++dh) {
-          float* const part = (float*)lds + (dh - dr) * kPart;  // [NW][32][PRS] (ring region)
-          if constexpr (!kOT) {
-            // dA^T: lane n holds row n, 4 consecutive d per 16-byte write
-            float* pw = part + (wid * 32 + (fresh_lane() & 31)) * PRS;
+          for (int dh = dr; dh < dr + DHR; ++dh) {
+            float* const part = (float*)lds + (dh - dr) * kPart;  // [NW][32][PRS] (ring region)
+            if constexpr (!kOT) {
+              // dA^T: lane n holds row n, 4 consecutive d per 16-byte write
+              float* pw = part + (wid * 32 + (fresh_lane() & 31)) * PRS;
 #pragma unroll
-            for (int dbl = 0; dbl < 2; ++dbl)
+              for (int dbl = 0; dbl < 2; ++dbl)
 #pragma unroll
-              for (int q4 = 0; q4 < 4; ++q4) {
-                const int dd = 32 * dbl + 8 * q4 + 4 * half;
-                floatx4 qv;
-                if constexpr (F32) {
-                  qv = *(const floatx4*)(qrow + 4 * (64 * dh + dd));
-                } else {
-                  const bf16x4 qb4 = *(const bf16x4*)(qrow + 2 * (64 * dh + dd));
+                for (int q4 = 0; q4 < 4; ++q4) {
+                  const int dd = 32 * dbl + 8 * q4 + 4 * half;
+                  floatx4 qv;
+                  if constexpr (F32) {
+                    qv = *(const floatx4*)(vrow + 4 * (64 * dh + dd));
+                  } else {
+                    const bf16x4 qb4 = *(const bf16x4*)(vrow + 2 * (64 * dh + dd));
 #pragma unroll
-                  for (int e = 0; e < 4; ++e) qv[e] = (float)qb4[e];
-                }
-                floatx4 x;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) x[e] = row_ok ? qv[e] * dA[2 * dh + dbl][4 * q4 + e] : 0.f;
-                *(floatx4*)(pw + dd) = x;
-              }
-          } else {
-            // dA (lane = d): lane (i, half) holds column d = 64 dh + 32 dbl + i of
-            // rows n = 8 g + 4 half + e; one q value per column
-            const int lf = fresh_lane();
-            const int hf = lf >> 5, i = lf & 31;
-            float* pw = part + wid * 32 * PRS + i;
-#pragma unroll
-            for (int dbl = 0; dbl < 2; ++dbl) {
-              const float qv = (float)*(const bf16*)(qrow + 2 * (64 * dh + 32 * dbl + i));
-              if (nv >= 32) {
-#pragma unroll
-                for (int g4 = 0; g4 < 4; ++g4)
-#pragma unroll
-                  for (int e = 0; e < 4; ++e)
-                    pw[(8 * g4 + 4 * hf + e) * PRS + 32 * dbl] = qv * dA[2 * dh + dbl][4 * g4 + e];
-              } else {
-                int nvm = nv;
-                asm volatile("" : "+s"(nvm));
-#pragma unroll
-                for (int g4 = 0; g4 < 4; ++g4)
-#pragma unroll
-                  for (int e = 0; e < 4; ++e) {
-                    const int nr_ = 8 * g4 + 4 * hf + e;
-                    pw[nr_ * PRS + 32 * dbl] = nr_ < nvm ? qv * dA[2 * dh + dbl][4 * g4 + e] : 0.f;
+                    for (int e = 0; e < 4; ++e) qv[e] = (float)qb4[e];
                   }
+                  floatx4 x;
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) x[e] = row_ok ? qv[e] * X[2 * dh + dbl][4 * q4 + e] : 0.f;
+                  *(floatx4*)(pw + dd) = x;
+                }
+            } else {
+              // dA (lane = d): lane (i, half) holds column d = 64 dh + 32 dbl + i of
+              // rows n = 8 g + 4 half + e; one q value per column
+              const int lf = fresh_lane();
+              const int hf = lf >> 5, i = lf & 31;
+              float* pw = part + wid * 32 * PRS + i;
+#pragma unroll
+              for (int dbl = 0; dbl < 2; ++dbl) {
+                const float qv = (float)*(const bf16*)(vrow + 2 * (64 * dh + 32 * dbl + i));
+                if (nv >= 32) {
+#pragma unroll
+                  for (int g4 = 0; g4 < 4; ++g4)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                      pw[(8 * g4 + 4 * hf + e) * PRS + 32 * dbl] = qv * X[2 * dh + dbl][4 * g4 + e];
+                } else {
+                  int nvm = nv;
+                  asm volatile("" : "+s"(nvm));
+#pragma unroll
+                  for (int g4 = 0; g4 < 4; ++g4)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                      const int nr_ = 8 * g4 + 4 * hf + e;
+                      pw[nr_ * PRS + 32 * dbl] = nr_ < nvm ? qv * X[2 * dh + dbl][4 * g4 + e] : 0.f;
+                    }
+                }
               }
             }
           }
-        }
-        block_barrier();  // every wave's rows staged
-        // thread index from a fresh lane id: the store addresses are not
-        // hoisted into registers held through the key loop
-        for (int o = fresh_lane() + 64 * wid; o < DHR * ROWS1 * 16; o += 64 * NW) {
-          const int u = DHR > 1 ? o / (ROWS1 * 16) : 0;
-          const int jrow = (DHR > 1 ? o % (ROWS1 * 16) : o) >> 4, d4 = o & 15;
-          const float* const part = (const float*)lds + u * kPart;
-          floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+          block_barrier();  // every wave's rows staged
+          // thread index from a fresh lane id: the store addresses are not
+          // hoisted into registers held through the key loop
+          for (int o = fresh_lane() + 64 * wid; o < DHR * ROWS1 * 16; o += 64 * NW) {
+            const int u = DHR > 1 ? o / (ROWS1 * 16) : 0;
+            const int jrow = (DHR > 1 ? o % (ROWS1 * 16) : o) >> 4, d4 = o & 15;
+            const float* const part = (const float*)lds + u * kPart;
+            floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int w = 0; w < NW; ++w) {
-            const int nn = w / NH + 31 - jrow;  // wave w = (qo, hw) = (w / NH, w % NH)
-            if (nn >= 0 && nn < 32) acc += *(const floatx4*)(part + (w * 32 + nn) * PRS + 4 * d4);
+            for (int w = 0; w < NW; ++w) {
+              const int nn = w / NH + 31 - jrow;  // wave w = (qo, hw) = (w / NH, w % NH)
+              if (nn >= 0 && nn < 32) acc += *(const floatx4*)(part + (w * 32 + nn) * PRS + 4 * d4);
+            }
+            *(floatx4*)(dst + jrow * DK + 64 * (dr + u) + 4 * d4) = acc;
           }
-          *(floatx4*)(dst + jrow * DK + 64 * (dr + u) + 4 * d4) = acc;
+          block_barrier();  // sums read before the next round (or exit) reuses the region
         }
-        block_barrier();  // sums read before the next round (or exit) reuses the region
-      }
+      };
+      const int64_t pofs = (((int64_t)hg * geo.qblocks + qb) * geo.nr + r) * (ROWS1 * DK);
+      write_partials(dA, qslot + wid * G::RSK, p.dk1p + pofs);  // the wave's q row
+      if constexpr (FV) write_partials(dO, qslot + NW * G::RSK + wid * G::RSV, p.dv1p + pofs);  // its dout row
     }
   }
 
@@ -693,7 +714,7 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_d
   }
 }
 
-template <int DK, int DV, int NQ, int NH, bool FUSE = false, bool F32 = false>
+template <int DK, int DV, int NQ, int NH, bool FUSE = false, bool F32 = false, bool FV = false>
 hipError_t launch_dq_t(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
   // one tile in flight: ring + short slot + q/dout rows stay <= 80 KB (2 per
   // CU; fp32 inputs: rows twice as wide, one per CU)
@@ -707,7 +728,7 @@ hipError_t launch_dq_t(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
   const size_t qslot = ((size_t)NW * (G::RSK + G::RSV) + 1023) / 1024 * 1024;
   const size_t ring = (size_t)(P + 1) * G::SLOT, red = (size_t)NW * 64 * 36 * sizeof(float);
   const size_t lds = (ring > red ? ring : red) + G::SLOT + qslot;
-  auto kern = bwd_dq_mfma_kernel<DK, DV, NQ, NH, P, FUSE, F32>;
+  auto kern = bwd_dq_mfma_kernel<DK, DV, NQ, NH, P, FUSE, F32, FV>;
   hipError_t e = set_lds_limit((const void*)kern, lds);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(geo.nblocks), dim3(64 * NW), lds, stream, p, geo);
@@ -716,6 +737,13 @@ hipError_t launch_dq_t(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
 
 template <int DK, int DV, bool F32 = false>
 hipError_t launch_dq_d(const BwdParams& p, BwdGeo geo, hipStream_t stream) {
+  if constexpr (F32) {
+    if (p.dk1p && p.dv1p) {  // dk1 and dv1 partials
+      if (p.group % 4 == 0) return launch_dq_t<DK, DV, 1, 4, true, true, true>(p, geo, stream);
+      if (p.group % 2 == 0) return launch_dq_t<DK, DV, 2, 2, true, true, true>(p, geo, stream);
+      return launch_dq_t<DK, DV, 4, 1, true, true, true>(p, geo, stream);
+    }
+  }
   if (p.group % 4 == 0)
     return p.dk1p ? launch_dq_t<DK, DV, 1, 4, true, F32>(p, geo, stream)
                   : launch_dq_t<DK, DV, 1, 4, false, F32>(p, geo, stream);
@@ -1913,6 +1941,17 @@ hipError_t launch_bwd_dk1_sum(const BwdParams& p, hipStream_t stream) {
   else if (p.d == 128) hipLaunchKernelGGL(bwd_dk1_sum_kernel<128>, grid, dim3(256), 0, stream, p, qblocks, nq, hsub, nr);
   else hipLaunchKernelGGL(bwd_dk1_sum_kernel<256>, grid, dim3(256), 0, stream, p, qblocks, nq, hsub, nr);
   return hipGetLastError();
+}
+
+hipError_t launch_bwd_dv1_sum(const BwdParams& p, hipStream_t stream) {
+  // the dk1 sum over the dv1 partials, into dv1 (value width and strides)
+  BwdParams q = p;
+  q.dk1p = p.dv1p;
+  q.dk1 = p.dv1;
+  q.dk_st = p.dv_st;
+  q.dk_sh = p.dv_sh;
+  q.d = p.dv;
+  return launch_bwd_dk1_sum(q, stream);
 }
 
 hipError_t launch_bwd_dkv2_mfma(const BwdParams& p, hipStream_t stream) {

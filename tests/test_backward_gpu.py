@@ -578,6 +578,51 @@ def test_backward_c4_full_size_dk1_partials_match_separate_pass(cuda, monkeypatc
             assert err <= bound, name
 
 
+def test_backward_fp32_dv1_partials_match_separate_pass(cuda, monkeypatch):
+    """The reference DeepSeek-V4.1 adapter shape in fp32 (B2 S8192, Hq 8 / Hkv 2,
+    D 128, windows 32 x 512): dk1 and dv1 from the dq pass's partials agree
+    with the separate dk1 / dv1 pass to fp32 precision (a different summation
+    order), dk2 and dv2 come from the same kernel either way (bitwise equal),
+    dq from the same arithmetic, and a second call is bitwise identical."""
+    import archlab_amd.architectures.simplicial_attention as shim
+    from archlab_amd import simplicial_attention
+    from archlab_amd import workloads as W
+    cfg = W.DSV41
+    q, k1, k2, v1, v2, _ = W.prefill_inputs(cfg, device=cuda)
+    g = torch.Generator("cpu").manual_seed(5)
+    dout = torch.randn(q.shape[:-1] + (v1.shape[-1],), generator=g).to(cuda)
+
+    def grads():
+        xd = [t.detach().clone().requires_grad_(True) for t in (q, k1, k2, v1, v2)]
+        out = simplicial_attention(*xd, cfg.w2, cfg.w1, scale=1.0)
+        out.backward(dout)
+        return [t.grad for t in xd]
+
+    fused = grads()
+    again = grads()
+    for name, a, b in zip(("dq", "dk1", "dk2", "dv1", "dv2"), fused, again):
+        assert torch.equal(a, b), name
+    real_empty = torch.empty
+
+    def empty(*size, **kw):  # refuse the workspace that holds the partials (1.1 GB here)
+        n = size[0] if size and isinstance(size[0], int) else None
+        if kw.get("dtype") is torch.uint8 and n is not None and n > (256 << 20):
+            raise torch.cuda.OutOfMemoryError("workspace refused by the test")
+        return real_empty(*size, **kw)
+
+    monkeypatch.setattr(shim.torch, "empty", empty)
+    separate = grads()
+    monkeypatch.undo()
+    for name, a, b in zip(("dq", "dk1", "dk2", "dv1", "dv2"), fused, separate):
+        err = (a - b).abs().max().item()
+        bound = 1e-5 * max(b.abs().max().item(), 1.0)
+        print(f"DSV41 fp32 fused vs separate dk1 / dv1 {name}: {err:.2e} / {bound:.1e}", flush=True)
+        if name in ("dk2", "dv2"):
+            assert torch.equal(a, b), name
+        else:
+            assert err <= bound, name
+
+
 @pytest.mark.parametrize("name", ["NS", "DSV41-bf16", "DSV41"])
 def test_backward_full_size_matches_portable(cuda, name):
     """Full-size workloads, the matrix-core backward against the portable
