@@ -28,9 +28,10 @@
  *   sa_prefill_bwd_workspace_bytes  size of its workspace: the per-(token,
  *                             head) delta and dlse rows and, for bf16 calls
  *                             whose short window is one 32-row group, the
- *                             dk1 partials written by the dq pass (at most
- *                             8 GiB; beyond that, or with
- *                             SA_FLAG_SEPARATE_DK1, a separate dk1 pass runs).
+ *                             dk1 partials written by the dq pass (fp32:
+ *                             dk1 and dv1 partials; at most 8 GiB; beyond
+ *                             that, or with SA_FLAG_SEPARATE_DK1, a separate
+ *                             dk1 / dv1 pass runs).
  *
  * Conventions
  *   - All pointers are device pointers; strides are in ELEMENTS; the last
@@ -192,7 +193,9 @@ typedef struct sa_prefill_bwd_args {
  *   value_dim each 64 or 128, or head_dim 256 over value_dim 128 / 256, short
  *   window <= 64; fp32 with head_dim == value_dim in {64, 128}, short window
  *   <= 32): 16-17.5x the bytes of q per 32 keys of short window, up to 8 GiB;
- *   none with SA_FLAG_SEPARATE_DK1 in args->fwd.flags;
+ *   none with SA_FLAG_SEPARATE_DK1 in args->fwd.flags; fp32 calls also hold
+ *   the dq pass's dv1 partials, the same size at value_dim (dk1 and dv1
+ *   partials together up to 8 GiB, else the dv1 pass runs);
  * - for short windows of 65-128 (33-64 at head_dim 256), the fp32 dk2 and dv2
  *   sums of the first of two dk2 / dv2 launches ([tokens][heads_kv][head_dim +
  *   value_dim]);

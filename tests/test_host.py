@@ -346,7 +346,9 @@ def test_backward_workspace_reserves_dk1_partials_for_fused_shapes(dtype, hq, hk
     short window <= 64; fp32 with equal widths of 64 or 128, short window
     <= 32), the partials: 31 + NQ fp32 rows of D per dq workgroup of NQ
     queries x 4 / NQ heads (NQ = 4, 2, 1 for GQA groups that are odd, even,
-    multiples of 4) and per 32-row group of short keys."""
+    multiples of 4) and per 32-row group of short keys; fp32 calls the dv1
+    partials as well (the same rows at the value width), while the two
+    together stay within 8 GiB."""
     from archlab_amd import _native
     lib = _native.load()
     tokens = 1001
@@ -375,7 +377,16 @@ def test_backward_workspace_reserves_dk1_partials_for_fused_shapes(dtype, hq, hk
     f32_mfma = dtype == "f32" and d == dv and d in (64, 128) and ws <= 32
     split = 2 * ((tokens * hk * d * 4 + 255) // 256 * 256) if f32_mfma else 0
     walk = _walk_split_bytes(dtype, tokens, hk, d, dv, ws, 512)
-    assert lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args)) == 2 * rows + part + dkv2 + split + walk
+    vpart = part // d * dv if fused and dtype == "f32" else 0  # dv1 partials (fp32)
+    assert lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args)) == 2 * rows + part + dkv2 + split + walk + vpart
+    if fused and dtype == "f32":
+        # dk1 partials of ~6 GiB: both together would pass 8 GiB, so only dk1's are reserved
+        mid = int((6 << 30) / per_query) // 4 * 4
+        args.fwd.total_tokens = args.fwd.seqlen = mid
+        rows_m = (mid * hq * 4 + 255) // 256 * 256
+        part_m = (-(-mid // nq) * (hq // (4 // nq)) * nr * (31 + nq) * d * 4 + 255) // 256 * 256
+        split_m = 2 * ((mid * hk * d * 4 + 255) // 256 * 256)
+        assert lib.sa_prefill_bwd_workspace_bytes(ctypes.byref(args)) == 2 * rows_m + part_m + split_m
     if fused:
         # past 8 GiB of partials the separate dk1 pass runs: no partials reserved
         big = int((8 << 30) / per_query) // 4 * 4 + 8
