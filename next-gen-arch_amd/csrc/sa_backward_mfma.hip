@@ -628,7 +628,7 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_d
           for (int dh = dr; dh < dr + DHR; ++dh) {
             float* const part = (float*)lds + (dh - dr) * kPart;  // [NW][32][PRS] (ring region)
             if constexpr (!kOT) {
-              // dA^T: lane n holds row n, 4 consecutive d per 16-byte write
+              // X^T (dA^T or O''^T): lane n holds row n, 4 consecutive d per 16-byte write
               float* pw = part + (wid * 32 + (fresh_lane() & 31)) * PRS;
 #pragma unroll
               for (int dbl = 0; dbl < 2; ++dbl)
@@ -649,7 +649,7 @@ __global__ __launch_bounds__(64 * NQ * NH, (DK > 128 || F32) ? 1 : 2) void bwd_d
                   *(floatx4*)(pw + dd) = x;
                 }
             } else {
-              // dA (lane = d): lane (i, half) holds column d = 64 dh + 32 dbl + i of
+              // X (lane = d; dk1 only): lane (i, half) holds column d = 64 dh + 32 dbl + i of
               // rows n = 8 g + 4 half + e; one q value per column
               const int lf = fresh_lane();
               const int hf = lf >> 5, i = lf & 31;
