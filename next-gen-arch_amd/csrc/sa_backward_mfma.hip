@@ -204,15 +204,25 @@ struct BwdOps {
     const int e_src = i16 >> 2, q_src = i16 & 3;
     const uint32_t vp = lds_addr(tile + (row0 + 4 * half + e_src) * RS + 32 * g16 + 8 * q_src);
     constexpr int kSteps = 2 * (D / 32);
+    // the fragments of step s+1 are read while step s's MFMAs run (the fp32
+    // passes hold one wave per SIMD: nothing else hides the LDS latency)
+    shortx4 h1[kSteps], h2[kSteps], l1[kSteps], l2[kSteps];
+    auto rd = [&](auto st) {
+      constexpr int s = decltype(st)::value;
+      RB::template vread<RS, s>(vp, h1[s], h2[s]);
+      RB::template vread<RS, s, 2 * D>(vp, l1[s], l2[s]);
+    };
+    rd(std::integral_constant<int, 0>{});
     static_for<0, kSteps>([&](auto st) {
       constexpr int s = decltype(st)::value;
-      shortx4 h1, h2, l1, l2;
-      RB::template vread<RS, s>(vp, h1, h2);
-      RB::template vread<RS, s, 2 * D>(vp, l1, l2);
-      lds_wait(h1, h2);
-      lds_wait(l1, l2);
-      const bf16x8 vh = __builtin_bit_cast(bf16x8, shortx8{h1[0], h1[1], h1[2], h1[3], h2[0], h2[1], h2[2], h2[3]});
-      const bf16x8 vl = __builtin_bit_cast(bf16x8, shortx8{l1[0], l1[1], l1[2], l1[3], l2[0], l2[1], l2[2], l2[3]});
+      if constexpr (s + 1 < kSteps) rd(std::integral_constant<int, s + 1>{});
+      constexpr int later = s + 1 < kSteps ? 4 : 0;  // reads issued after step s's
+      lds_wait_n<later>(h1[s], h2[s]);
+      lds_wait_n<later>(l1[s], l2[s]);
+      const bf16x8 vh =
+          __builtin_bit_cast(bf16x8, shortx8{h1[s][0], h1[s][1], h1[s][2], h1[s][3], h2[s][0], h2[s][1], h2[s][2], h2[s][3]});
+      const bf16x8 vl =
+          __builtin_bit_cast(bf16x8, shortx8{l1[s][0], l1[s][1], l1[s][2], l1[s][3], l2[s][0], l2[s][1], l2[s][2], l2[s][3]});
       const bf16x8& bh = s / (D / 32) == 0 ? pb0 : pb1;
       const bf16x8& bl = s / (D / 32) == 0 ? pl0 : pl1;
       __builtin_amdgcn_sched_barrier(0);
