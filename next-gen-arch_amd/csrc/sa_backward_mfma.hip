@@ -173,24 +173,30 @@ struct BwdOps {
   __device__ static __forceinline__ floatx16 rows_x_hl(const char* tile, int row0, int lane, const bf16x8* x,
                                                        const bf16x8* xl) {
     const int n = lane & 31, half = lane >> 5;
-    const char* kp = tile + (row0 + n) * RS + 16 * half;
+    const uint32_t ka = lds_addr(tile + (row0 + n) * RS + 16 * half);
     floatx16 c = floatx16{};
-    bf16x8 fh = *(const bf16x8*)kp, fl = *(const bf16x8*)(kp + 2 * D);
-#pragma unroll
-    for (int t = 0; t < D / 16; ++t) {
-      bf16x8 nh, nl;
-      if (t + 1 < D / 16) {
-        nh = *(const bf16x8*)(kp + 32 * (t + 1));
-        nl = *(const bf16x8*)(kp + 2 * D + 32 * (t + 1));
-      }
+    // hi and lo fragments read two steps ahead with counted waits (the
+    // compiler's own waits would also wait for the reads issued ahead)
+    constexpr int T = D / 16, KA = T < 2 ? T : 2;
+    bf16x8 fh[T], fl[T];
+    auto rd = [&](auto tt) {
+      constexpr int t = decltype(tt)::value;
+      fh[t] = ds_read_b128_at<32 * t>(ka);
+      fl[t] = ds_read_b128_at<2 * D + 32 * t>(ka);
+    };
+    static_for<0, KA>([&](auto tt) { rd(tt); });
+    static_for<0, T>([&](auto tt) {
+      constexpr int t = decltype(tt)::value;
+      if constexpr (t + KA < T) rd(std::integral_constant<int, t + KA>{});
+      constexpr int later = 2 * ((t + KA < T ? t + KA : T - 1) - t);  // reads issued after step t's pair
+      lds_wait_k<later + 1>(fh[t]);
+      lds_wait_k<later>(fl[t]);
       __builtin_amdgcn_sched_barrier(0);
-      c = mfma32x32x16(fh, x[t], c);
-      c = mfma32x32x16(fh, xl[t], c);
-      c = mfma32x32x16(fl, x[t], c);
+      c = mfma32x32x16(fh[t], x[t], c);
+      c = mfma32x32x16(fh[t], xl[t], c);
+      c = mfma32x32x16(fl[t], x[t], c);
       __builtin_amdgcn_sched_barrier(0);
-      fh = nh;
-      fl = nl;
-    }
+    });
     return c;
   }
 
